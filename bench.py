@@ -1,0 +1,236 @@
+#!/usr/bin/env python
+"""Benchmark of the BASELINE metric: attention forward effective TFLOP/s and %
+of MI355X dense bf16 MFMA peak, on one GPU.
+
+Default workload = BASELINE config 2 (the headline shape): bf16, B=1,
+Lq=Lk=8192, H=16, D=64, non-causal, default scale, q/k/v ~ N(0,1) from seed 1
+(the reference test recipe, tests/test_flash_attn_func.py:52-57).  One step =
+one `flash_attn_func` forward over inputs already resident in HBM.
+
+Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
+  roofline     : the dominant kernel's algorithmic FLOPs / its average launch
+                 time (HIP events around each launch on the launch stream),
+                 against the dense bf16 MFMA peak (2.5 PFLOP/s);
+  cpu_baseline : the reference's chunked-fp32 torch path (oracle/chunked.py)
+                 timed on this host's cores on a bounded sample of the same
+                 workload (a subset of heads).
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+METRIC = "attn fwd effective TFLOP/s + % MFMA peak, bf16 H=16 D=64/128 L=8k, 1 MI355X"
+PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA
+# HBM bytes per launch measured by rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE, scaled
+# by the copy-kernel calibration factor) for the default workload; None until
+# measured.  See profiles/ for the runs these come from.
+TRAFFIC_BYTES = {}
+
+
+def make_config(cfg: int):
+    import torch
+
+    dev = "cuda"
+    if cfg == 2:
+        g = torch.Generator().manual_seed(1)
+        B, L, H, D = 1, 8192, 16, 64
+        q, k, v = (torch.randn(B, L, H, D, generator=g) for _ in range(3))
+        q, k, v = (t.to(dev, torch.bfloat16) for t in (q, k, v))
+        kw = dict(causal=False)
+        pairs = B * H * L * L
+        return dict(q=q, k=k, v=v, kw=kw, dtype="bf16", D=D, formula=4 * B * H * L * L * D,
+                    algo=4 * pairs * D, varlen=None,
+                    workload="cfg2: bf16 B=1 Lq=Lk=8192 H=16 D=64 non-causal, seed 1")
+    if cfg == 3:
+        g = torch.Generator().manual_seed(2)
+        B, L, H, D = 1, 8192, 16, 128
+        q, k, v = (torch.randn(B, L, H, D, generator=g) for _ in range(3))
+        q, k, v = (t.to(dev, torch.float16) for t in (q, k, v))
+        pairs = B * H * L * (L + 1) // 2
+        return dict(q=q, k=k, v=v, kw=dict(causal=True), dtype="fp16", D=D, formula=4 * B * H * L * L * D // 2,
+                    algo=4 * pairs * D, varlen=None,
+                    workload="cfg3: fp16 B=1 Lq=Lk=8192 H=16 D=128 causal, seed 2")
+    if cfg == 4:
+        g = torch.Generator().manual_seed(3)
+        lens = torch.randint(256, 4097, (8,), generator=g)
+        T = int(lens.sum())
+        q = torch.randn(T, 32, 128, generator=g).to(dev, torch.bfloat16)
+        k = torch.randn(T, 8, 128, generator=g).to(dev, torch.bfloat16)
+        v = torch.randn(T, 8, 128, generator=g).to(dev, torch.bfloat16)
+        cu = torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)]).to(torch.int32).to(dev)
+        Ls = [int(x) for x in lens]
+        pairs = sum(32 * L * (L + 1) // 2 for L in Ls)
+        formula = sum(4 * 32 * L * L * 128 // 2 for L in Ls)
+        return dict(q=q, k=k, v=v, kw=dict(causal=True), dtype="bf16", D=128, formula=formula,
+                    algo=4 * pairs * 128, varlen=(cu, max(Ls)),
+                    workload=f"cfg4: bf16 varlen lens={Ls} Hq=32 Hkv=8 D=128 causal, seed 3")
+    if cfg == 5:
+        g = torch.Generator().manual_seed(4)
+        B, L, H, D = 1, 32768, 16, 128
+        q, k, v = (torch.randn(B, L, H, D, generator=g) * 0.5 for _ in range(3))
+        q, k, v = (t.to(dev, torch.bfloat16) for t in (q, k, v))
+        slopes = torch.tensor([2 ** (-8 * (i + 1) / 16) for i in range(H)], dtype=torch.float32, device=dev)
+        # valid pairs per head: keys j in [i-2048, i]
+        pairs = B * H * sum(min(i, 2048) + 1 for i in range(L))
+        return dict(q=q, k=k, v=v, kw=dict(causal=True, window_size=(2048, 0), softcap=30.0, alibi_slopes=slopes),
+                    dtype="bf16", D=D, formula=4 * B * H * L * L * D // 2, algo=4 * pairs * D, varlen=None,
+                    workload="cfg5: bf16 B=1 L=32768 H=16 D=128 causal window=(2048,0) softcap=30 ALiBi, seed 4")
+    raise SystemExit(f"unknown config {cfg}")
+
+
+def run_step(c):
+    import mtlflashattn_amd as mfa
+
+    if c["varlen"] is not None:
+        cu, mx = c["varlen"]
+        return mfa.flash_attn_varlen_func(c["q"], c["k"], c["v"], cu, cu, mx, mx, **c["kw"])
+    return mfa.flash_attn_func(c["q"], c["k"], c["v"], **c["kw"])
+
+
+def cpu_baseline(cfg: int, budget_s: float = 12.0):
+    """Oracle (reference chunked-fp32 torch path) on host cores, bounded sample."""
+    import torch
+
+    from oracle import chunked
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = make_config(cfg)
+    if c["varlen"] is not None:
+        # one sequence of the batch (the shortest), all heads
+        cu, _ = c["varlen"]
+        cu = cu.cpu().tolist()
+        i = min(range(len(cu) - 1), key=lambda j: cu[j + 1] - cu[j])
+        q, k, v = (t[cu[i]:cu[i + 1]].cpu() for t in (c["q"], c["k"], c["v"]))
+        L = cu[i + 1] - cu[i]
+        fn = lambda: chunked.flash_attn_varlen_func(q, k, v, [0, L], [0, L], causal=True)  # noqa: E731
+        flops = 4 * 32 * L * L * 128 // 2
+        sample = f"sequence {i} (L={L}) of the varlen batch, all 32 heads"
+    else:
+        q, k, v = (t.cpu() for t in (c["q"], c["k"], c["v"]))
+        H = q.shape[2]
+        heads = 1
+        kw = {kk: (vv.cpu() if hasattr(vv, "cpu") else vv) for kk, vv in c["kw"].items()}
+        t0 = time.perf_counter()
+        rows = None
+        if cfg == 5:
+            rows = {q.shape[1] - 2048}  # last 2048-row chunk, full key range computed by the oracle
+        chunked.flash_attn_func(q[:, :, :1], k[:, :, :1], v[:, :, :1], alibi_slopes=None if "alibi_slopes" not in kw
+                                else kw["alibi_slopes"][:1], rows=rows,
+                                **{kk: vv for kk, vv in kw.items() if kk != "alibi_slopes"})
+        one = time.perf_counter() - t0
+        heads = max(1, min(H, int(budget_s / 3 / max(one, 1e-3))))
+        qs, ks, vs = q[:, :, :heads], k[:, :, :heads], v[:, :, :heads]
+        kws = {kk: vv for kk, vv in kw.items() if kk != "alibi_slopes"}
+        al = kw["alibi_slopes"][:heads] if "alibi_slopes" in kw else None
+        fn = lambda: chunked.flash_attn_func(qs, ks, vs, alibi_slopes=al, rows=rows, **kws)  # noqa: E731
+        L = q.shape[1]
+        nrows = 2048 if rows else L
+        flops = 4 * heads * nrows * L * c["D"] // (2 if (c["kw"].get("causal") and not rows) else 1)
+        sample = f"{heads} of {H} heads" + (", last 2048 query rows" if rows else ", all rows") + \
+            f" (full Lq x Lk grid computed, as the reference torch path does)"
+    fn()  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": sample, "seconds": round(med, 3),
+            "note": "formula FLOPs of the sample (4*H*Lq*Lk*D, halved for causal) / median of 3 runs"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "bench.py measures one GPU only: this build's path is single-GPU "
+                                   "(head/sequence sharding across GPUs is a design note, not built); "
+                                   f"--gpus {args.gpus} is not supported"}))
+        sys.exit(2)
+
+    import torch
+
+    from mtlflashattn_amd import _kernel
+
+    c = make_config(args.config)
+    for _ in range(args.warmup):
+        run_step(c)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    # whole-job timing: K back-to-back steps
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    t_start.record(stream)
+    for _ in range(args.steps):
+        run_step(c)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = t_start.elapsed_time(t_end)
+    ms_step = ms_total / args.steps
+    # per-launch kernel time: events bracketing each launch on its stream
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in evs:
+        a.record(stream)
+        run_step(c)
+        b.record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+
+    value = c["formula"] / (ms_step / 1e3) / 1e12
+    peak = PEAK_TFLOPS[c["dtype"]]
+    achieved = c["algo"] / (kernel_ms / 1e3) / 1e12
+    if c["varlen"] is not None:
+        info = None
+        kname = "mfa_fwd16 (varlen)"
+    else:
+        info = _kernel.launch_info(c["q"], c["k"], c["v"], causal=c["kw"].get("causal", False),
+                                   softcap=c["kw"].get("softcap", 0.0),
+                                   alibi="alibi_slopes" in c["kw"],
+                                   window_left=c["kw"].get("window_size", (-1, -1))[0],
+                                   window_right=c["kw"].get("window_size", (-1, -1))[1])
+        kname = info.kernel_name.decode()
+    traffic = TRAFFIC_BYTES.get(args.config)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": c["dtype"],
+        "data": "synthetic (seeded randn, reference recipe)",
+        "config": {"workload": c["workload"], "pct_mfma_peak": round(100 * value / peak, 2),
+                   "formula_flops": c["formula"], "algorithmic_flops": c["algo"]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kname,
+                     "kernel_ms": round(kernel_ms, 4),
+                     "note": "algorithmic FLOPs (4*D per valid (query,key) pair) / mean launch time"},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.config)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

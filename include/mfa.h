@@ -1,0 +1,156 @@
+/*
+ * mfa.h -- C ABI of the MI355X (gfx950) flash-attention forward library
+ * (libmtlfa_hip.so, built from mtlflashattn_amd/csrc/mfa_fwd.hip).
+ *
+ * This is the drop-in boundary that replaces the reference's per-tier Metal
+ * launch calls.  In the reference the Python launcher binds a JIT-compiled
+ * Metal library and calls one kernel per tier with device buffers Q, K, V, O
+ * plus three small parameter tensors:
+ *   SH  int32 shape vector   [B, Hq, Hkv, Lq, Lk, causal(, Lkp)]
+ *   PR  fp32 parameter vector [scale, softcap, win_left, win_right, alibi_on]
+ *   AL  fp32 [B*Hq] ALiBi slopes (or a 1-element dummy)
+ * (metal_flash_attn/_kernel.py:1309-1312 `lib.flash_attn_fwd_v2r_dtype(...)`,
+ *  :1333-1337, :1368-1373, :1397-1401, :1416-1419; SH/PR/AL semantics at
+ *  :1221-1272).  Here the same information travels in one POD struct, passed
+ * by pointer and copied by value into the kernel arguments, so no per-call
+ * device parameter tensors exist at all.
+ *
+ * Contract:
+ *  - Every entry point is stateless and re-entrant.  mfa_fwd only enqueues
+ *    work on `stream` (a hipStream_t, e.g. torch.cuda.current_stream()
+ *    .cuda_stream); it never synchronizes and never allocates.
+ *  - Return value 0 = success, negative = error; the message is available
+ *    from mfa_last_error() on the same thread.
+ *  - All pointers are device pointers.  The head dimension must be
+ *    contiguous (element stride 1) in q, k, v and o; every other stride is an
+ *    element stride and may be arbitrary (views, packed qkv, heads-second or
+ *    heads-third layouts).
+ */
+#ifndef MTLFA_MFA_H
+#define MTLFA_MFA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MFA_ABI_VERSION 1
+
+/* element types (dtype_in / dtype_out) */
+#define MFA_DTYPE_F16 0
+#define MFA_DTYPE_BF16 1
+#define MFA_DTYPE_F32 2
+
+/* error codes */
+#define MFA_OK 0
+#define MFA_ERR_INVALID -1     /* bad argument (shape, stride, alignment, dtype) */
+#define MFA_ERR_UNSUPPORTED -2 /* valid request this build does not implement */
+#define MFA_ERR_LAUNCH -3      /* the HIP runtime refused the launch */
+
+#define MFA_MAX_HEAD_DIM 128
+
+/*
+ * Forward parameters.  Replaces the SH/PR/AL buffers of the reference
+ * (metal_flash_attn/_kernel.py:1221-1272) and the heads-second tensor
+ * arguments of flash_attn_forward (metal_flash_attn/_kernel.py:1052-1053).
+ *
+ * Dense mode (cu_seqlens_q == NULL):
+ *   q [batch, seqlen_q, heads_q, head_dim] addressed through the q_*_stride
+ *   fields, likewise k/v [batch, seqlen_k, heads_kv, head_dim] and
+ *   o [batch, seqlen_q, heads_q, head_dim].
+ * Varlen mode (cu_seqlens_q != NULL, metal_flash_attn/__init__.py:102-183):
+ *   q [total_q, heads_q, head_dim], k/v [total_k, heads_kv, head_dim],
+ *   o [total_q, heads_q, head_dim]; sequence i owns tokens
+ *   [cu_seqlens_q[i], cu_seqlens_q[i+1]) of q/o and
+ *   [cu_seqlens_k[i], cu_seqlens_k[i+1]) of k/v.  `batch` is the number of
+ *   sequences, the *_batch_stride fields are ignored, and seqlen_q/seqlen_k
+ *   must hold max_seqlen_q/max_seqlen_k (upper bounds of every sequence).
+ *
+ * Masking/bias (metal_flash_attn/_kernel.py:32-87): for query row i of a
+ * sequence with Lq queries and Lk keys, center = i + (Lk - Lq); key j is
+ * valid iff j <= center (causal), j >= center - window_left (window_left >= 0)
+ * and j <= center + window_right (window_right >= 0).  Scores are
+ * s = scale * q.k; s = softcap * tanh(s / softcap) when softcap > 0;
+ * s -= slope * |center - j| when alibi_slopes != NULL, with
+ * slope = alibi_slopes[b * alibi_batch_stride + h] (alibi_batch_stride 0 for
+ * per-head [Hq] slopes, Hq for [B, Hq]).  Rows with no valid key produce 0.
+ */
+typedef struct mfa_fwd_params {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+
+    int64_t q_batch_stride, q_seq_stride, q_head_stride;
+    int64_t k_batch_stride, k_seq_stride, k_head_stride;
+    int64_t v_batch_stride, v_seq_stride, v_head_stride;
+    int64_t o_batch_stride, o_seq_stride, o_head_stride;
+
+    int32_t batch;
+    int32_t heads_q;
+    int32_t heads_kv;
+    int32_t seqlen_q;
+    int32_t seqlen_k;
+    int32_t head_dim;
+
+    const int32_t* cu_seqlens_q; /* NULL = dense */
+    const int32_t* cu_seqlens_k; /* NULL = dense */
+
+    float scale;
+    float softcap;        /* 0 = off; must be >= 0 */
+    int32_t window_left;  /* -1 = unbounded */
+    int32_t window_right; /* -1 = unbounded */
+    int32_t causal;       /* 0/1, bottom-right aligned */
+
+    const float* alibi_slopes; /* NULL = off; fp32 */
+    int32_t alibi_batch_stride;
+
+    int32_t dtype_in;  /* MFA_DTYPE_* of q, k and v */
+    int32_t dtype_out; /* == dtype_in, or MFA_DTYPE_F32 (full-precision output) */
+    int32_t reserved;
+} mfa_fwd_params;
+
+/* Launch geometry of one mfa_fwd call (for profiling/roofline reports). */
+typedef struct mfa_launch_info {
+    int32_t grid_x;          /* workgroups launched */
+    int32_t block_x;         /* threads per workgroup */
+    int32_t rows_per_block;  /* query rows per workgroup tile */
+    int32_t keys_per_block;  /* keys per K/V block */
+    int32_t lds_bytes;       /* LDS bytes per workgroup */
+    char kernel_name[96];    /* short name of the kernel instantiation */
+} mfa_launch_info;
+
+/* ABI version of the loaded library (MFA_ABI_VERSION).  No counterpart in
+ * the reference (its kernels are JIT-compiled from source strings). */
+int mfa_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none).  Replaces
+ * the RuntimeError strings of the reference's forced-tier checks
+ * (metal_flash_attn/_kernel.py:1083-1140). */
+const char* mfa_last_error(void);
+
+/* 1 if mfa_fwd implements (dtype_in, head_dim) on this build, else 0.
+ * Replaces the eligibility probes _v1_eligible/_v2_dtype_eligible
+ * (metal_flash_attn/_kernel.py:928-936, :896-912). */
+int mfa_supported(int32_t dtype_in, int32_t head_dim);
+
+/* Enqueue the attention forward on `stream` (hipStream_t; NULL = default
+ * stream).  Replaces the tier launchers _flash_v2r_dtype / _flash_v2_dtype /
+ * _flash_v2 / _flash_v1 / _flash_v0 (metal_flash_attn/_kernel.py:1288-1420)
+ * and their kernel calls. */
+int mfa_fwd(const mfa_fwd_params* params, void* stream);
+
+/* Fill *info with the geometry mfa_fwd would launch for `params`; enqueues
+ * nothing.  No counterpart in the reference. */
+int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info);
+
+/* sizeof(mfa_fwd_params) as compiled into the library, so FFI bindings can
+ * check their struct mirror.  No counterpart in the reference. */
+int mfa_params_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTLFA_MFA_H */

@@ -1,0 +1,191 @@
+"""MI355X-native flash-attention forward for PyTorch-ROCm -- CUDA flash-attn API surface.
+
+Drop-in for mtlflashattn's public API (metal_flash_attn/__init__.py): the same
+six functions, argument meanings and error contract.  Inference-only (no
+backward).  Unsupported features raise NotImplementedError so callers can fall
+back, rather than silently approximating (metal_flash_attn/__init__.py:1-5).
+
+Every call runs the gfx950 HIP kernels of libmtlfa_hip.so on the tensors'
+ROCm device; there is no CPU path.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ._kernel import MAX_HEAD_DIM, flash_attn_forward, forward_bshd, forward_varlen
+from ._version import __version__
+
+__all__ = [
+    "flash_attn_func",
+    "flash_attn_varlen_func",
+    "flash_attn_qkvpacked_func",
+    "flash_attn_kvpacked_func",
+    "flash_attn_varlen_qkvpacked_func",
+    "flash_attn_varlen_kvpacked_func",
+    "flash_attn_forward",
+    "__version__",
+]
+
+_SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, deterministic, return_attn_probs):
+    """Error contract of metal_flash_attn/__init__.py:28-59, checked in the same order."""
+    if dropout_p:
+        raise NotImplementedError("mtlflashattn_amd: dropout_p > 0 not supported (inference-only)")
+    if (
+        not isinstance(window_size, (tuple, list))
+        or len(window_size) != 2
+        or any(not isinstance(w, int) or isinstance(w, bool) or w < -1 for w in window_size)
+    ):
+        raise ValueError(
+            "mtlflashattn_amd: window_size must be a (left, right) pair of ints >= -1 "
+            "(-1 = unbounded on that side)"
+        )
+    if softcap < 0:
+        raise ValueError("mtlflashattn_amd: softcap must be >= 0 (0 disables capping)")
+    if alibi_slopes is not None and not torch.is_tensor(alibi_slopes):
+        raise TypeError("mtlflashattn_amd: alibi_slopes must be a tensor of per-head slopes")
+    if deterministic:
+        raise NotImplementedError("mtlflashattn_amd: deterministic not supported")
+    if return_attn_probs:
+        raise NotImplementedError("mtlflashattn_amd: return_attn_probs not supported (probs never materialized)")
+    if q.device.type != "cuda" or torch.version.hip is None:
+        raise NotImplementedError(f"mtlflashattn_amd: device {q.device.type!r} not supported (ROCm GPU only)")
+    if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise NotImplementedError(f"mtlflashattn_amd: dtype {q.dtype} (q/k/v must match, fp16/bf16/fp32)")
+    D = q.shape[-1]
+    if D > MAX_HEAD_DIM:
+        raise NotImplementedError(f"mtlflashattn_amd: head_dim {D} > {MAX_HEAD_DIM}")
+    if k.shape[-1] != D or v.shape[-1] != D:
+        raise ValueError("mtlflashattn_amd: q/k/v head_dim mismatch")
+
+
+def flash_attn_func(
+    q,
+    k,
+    v,
+    dropout_p=0.0,
+    softmax_scale=None,
+    causal=False,
+    window_size=(-1, -1),
+    softcap=0.0,
+    alibi_slopes=None,
+    deterministic=False,
+    return_attn_probs=False,
+):
+    """Drop-in for flash_attn.flash_attn_func (forward only; metal_flash_attn/__init__.py:62-99).
+
+    q: [B, Lq, Hq, D]; k, v: [B, Lk, Hkv, D] (heads-third, CUDA flash-attn layout).
+    Hkv must divide Hq (GQA/MQA). Returns [B, Lq, Hq, D] in q.dtype.
+    """
+    _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, deterministic, return_attn_probs)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError(f"mtlflashattn_amd: expected 4-D [B,S,H,D] tensors, got q.dim()={q.dim()}")
+    Hq, Hkv = q.shape[2], k.shape[2]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
+    if k.shape[1] != v.shape[1]:
+        raise ValueError("mtlflashattn_amd: k/v seqlen mismatch")
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    return forward_bshd(
+        q, k, v, scale=scale, causal=causal, softcap=softcap,
+        window_left=window_size[0], window_right=window_size[1], alibi_slopes=alibi_slopes,
+    )
+
+
+def flash_attn_varlen_func(
+    q,
+    k,
+    v,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    max_seqlen_q,
+    max_seqlen_k,
+    dropout_p=0.0,
+    softmax_scale=None,
+    causal=False,
+    window_size=(-1, -1),
+    softcap=0.0,
+    alibi_slopes=None,
+    deterministic=False,
+    return_attn_probs=False,
+    block_table=None,
+):
+    """Drop-in for flash_attn.flash_attn_varlen_func (forward only; metal_flash_attn/__init__.py:102-183).
+
+    q: [total_q, Hq, D]; k, v: [total_k, Hkv, D] packed without padding;
+    cu_seqlens_*: [B+1] int32 cumulative sequence lengths.
+    Returns [total_q, Hq, D] in q.dtype.  All sequences run in one launch.
+    """
+    _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, deterministic, return_attn_probs)
+    if block_table is not None:
+        raise NotImplementedError("mtlflashattn_amd: block_table (paged KV cache) not supported")
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError(f"mtlflashattn_amd: expected 3-D [total,H,D] tensors, got q.dim()={q.dim()}")
+    if cu_seqlens_q.shape[0] != cu_seqlens_k.shape[0]:
+        raise ValueError(
+            f"mtlflashattn_amd: cu_seqlens_q ({cu_seqlens_q.shape[0]}) and "
+            f"cu_seqlens_k ({cu_seqlens_k.shape[0]}) imply different batch sizes"
+        )
+    Hq, Hkv = q.shape[1], k.shape[1]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
+    if k.shape[0] != v.shape[0]:
+        raise ValueError("mtlflashattn_amd: k/v total token count mismatch")
+
+    # One host read of both prefix sums (the reference reads them for the same
+    # checks, metal_flash_attn/__init__.py:145-154); it also yields the true
+    # longest lengths, so a too-small max_seqlen_* cannot drop rows.
+    n = cu_seqlens_q.shape[0]
+    cu = torch.cat([cu_seqlens_q.reshape(-1).to(torch.int64), cu_seqlens_k.reshape(-1).to(torch.int64)]).tolist()
+    cu_q, cu_k = cu[:n], cu[n:]
+    if cu_q[-1] != q.shape[0]:
+        raise ValueError(f"mtlflashattn_amd: cu_seqlens_q[-1]={cu_q[-1]} != total_q={q.shape[0]}")
+    if cu_k[-1] != k.shape[0]:
+        raise ValueError(f"mtlflashattn_amd: cu_seqlens_k[-1]={cu_k[-1]} != total_k={k.shape[0]}")
+    lens_q = [b - a for a, b in zip(cu_q[:-1], cu_q[1:])]
+    lens_k = [b - a for a, b in zip(cu_k[:-1], cu_k[1:])]
+    if any(x < 0 for x in lens_q) or any(x < 0 for x in lens_k) or cu_q[0] != 0 or cu_k[0] != 0:
+        raise ValueError("mtlflashattn_amd: cu_seqlens must be non-decreasing prefix sums starting at 0")
+
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    return forward_varlen(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, max(lens_q, default=0), max(lens_k, default=0),
+        scale=scale, causal=causal, softcap=softcap, window_left=window_size[0],
+        window_right=window_size[1], alibi_slopes=alibi_slopes,
+    )
+
+
+def flash_attn_qkvpacked_func(qkv, *args, **kwargs):
+    """Drop-in for flash_attn.flash_attn_qkvpacked_func. qkv: [B, S, 3, H, D]."""
+    if qkv.dim() != 5 or qkv.shape[2] != 3:
+        raise ValueError(f"mtlflashattn_amd: expected qkv [B,S,3,H,D], got {tuple(qkv.shape)}")
+    q, k, v = qkv.unbind(dim=2)
+    return flash_attn_func(q, k, v, *args, **kwargs)
+
+
+def flash_attn_kvpacked_func(q, kv, *args, **kwargs):
+    """Drop-in for flash_attn.flash_attn_kvpacked_func. kv: [B, Sk, 2, Hkv, D]."""
+    if kv.dim() != 5 or kv.shape[2] != 2:
+        raise ValueError(f"mtlflashattn_amd: expected kv [B,S,2,H,D], got {tuple(kv.shape)}")
+    k, v = kv.unbind(dim=2)
+    return flash_attn_func(q, k, v, *args, **kwargs)
+
+
+def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, *args, **kwargs):
+    """Drop-in for flash_attn.flash_attn_varlen_qkvpacked_func. qkv: [total, 3, H, D]."""
+    if qkv.dim() != 4 or qkv.shape[1] != 3:
+        raise ValueError(f"mtlflashattn_amd: expected qkv [total,3,H,D], got {tuple(qkv.shape)}")
+    q, k, v = qkv.unbind(dim=1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, max_seqlen, max_seqlen, *args, **kwargs)
+
+
+def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, *args, **kwargs):
+    """Drop-in for flash_attn.flash_attn_varlen_kvpacked_func. kv: [total_k, 2, Hkv, D]."""
+    if kv.dim() != 4 or kv.shape[1] != 2:
+        raise ValueError(f"mtlflashattn_amd: expected kv [total,2,H,D], got {tuple(kv.shape)}")
+    k, v = kv.unbind(dim=1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, *args, **kwargs)

@@ -1,0 +1,306 @@
+"""Dispatcher boundary and HIP launcher.
+
+`flash_attn_forward` keeps the signature and contract of the reference's
+internal boundary (metal_flash_attn/_kernel.py:1052-1153): heads-second
+q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D] with any strides in, contiguous
+[B,Hq,Lq,D] in q.dtype out.  Behind it the reference's Metal tier dispatch
+(v0/v1/v2/v2r/v2_dtype, _kernel.py:716-985, :1288-1420) is replaced by one
+path: the C ABI of libmtlfa_hip.so (include/mfa.h), which launches the gfx950
+FA-2 kernels on torch's current HIP stream.
+
+There is no silent fallback: a tensor that is not on a ROCm GPU raises
+NotImplementedError (as the reference raises for non-MPS devices,
+metal_flash_attn/__init__.py:51-52) and a missing or broken HIP library
+raises RuntimeError.
+"""
+from __future__ import annotations
+
+import atexit
+import os
+import sys
+import warnings
+from collections import namedtuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _hip
+
+# Bias/masking knobs threaded through the launcher (metal_flash_attn/_kernel.py:20-24).
+# softcap: logit soft-cap (0 = off). window_left/window_right: sliding-window key
+# bounds relative to the bottom-right diagonal (-1 = open). alibi: fp32 slopes or None.
+_BiasParams = namedtuple("_BiasParams", "softcap window_left window_right alibi")
+
+MAX_HEAD_DIM = 128  # metal_flash_attn/_kernel.py:26
+
+_SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+# Every value the reference accepted for MTLFLASHATTN_KERNEL
+# (metal_flash_attn/_kernel.py:1077-1153) selects the single HIP path here.
+_KNOWN_MODES = frozenset(
+    {"auto", "hip", "torch", "pytorch", "v0", "v1", "v2", "v2_fp32", "v2_bf16", "v2_dtype", "v2_typed"}
+)
+_warned_modes = set()
+
+
+def _kernel_mode() -> str:
+    mode = os.environ.get("MTLFLASHATTN_KERNEL", "auto").lower()
+    if mode not in ("auto", "hip") and mode not in _warned_modes:
+        _warned_modes.add(mode)
+        what = "a Metal tier" if mode in _KNOWN_MODES else "unknown"
+        warnings.warn(
+            f"mtlflashattn_amd: MTLFLASHATTN_KERNEL={mode!r} is {what}; the ROCm build has a single HIP "
+            "path and uses it for every mode",
+            stacklevel=3,
+        )
+    return "hip"
+
+
+# ---------------------------------------------------------------------------
+# trace (metal_flash_attn/_kernel.py:988-1049): per-(dtype, D, Lq, Lk, causal,
+# label) call counts, printed to stderr at exit when MTLFLASHATTN_TRACE is set.
+
+_trace = {}
+
+
+def _trace_enabled() -> bool:
+    return os.environ.get("MTLFLASHATTN_TRACE", "").lower() in ("1", "on", "true", "yes")
+
+
+def _effective_kernel_label(q, k, v) -> str:
+    """Label of the path flash_attn_forward takes (one path: the HIP kernels)."""
+    return "hip"
+
+
+def _record_trace(dtype, D, Lq, Lk, causal, label="hip"):
+    try:
+        key = (str(dtype).replace("torch.", ""), int(D), int(Lq), int(Lk), bool(causal), label)
+        _trace[key] = _trace.get(key, 0) + 1
+    except Exception:
+        pass  # tracing must never break a real run
+
+
+def _trace_summary_lines():
+    if not _trace:
+        return []
+    total = sum(_trace.values())
+    lines = [f"[MTLFLASHATTN_TRACE] {total} attention call(s), {len(_trace)} distinct shape/kernel combos:"]
+    for (dt, D, Lq, Lk, causal, label), n in sorted(_trace.items(), key=lambda kv: (-kv[1], kv[0])):
+        lines.append(
+            f"  calls={n:<6} {dt:<9} D={D:<4} Lq={Lq:<6} Lk={Lk:<6} causal={'T' if causal else 'F'}  -> {label}"
+        )
+    return lines
+
+
+@atexit.register
+def _trace_atexit():
+    if _trace_enabled() and _trace:
+        print("\n".join(_trace_summary_lines()), file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# argument preparation
+
+
+def _alibi_arg(alibi_slopes, B, Hq, device):
+    """Validate [Hq] / [B, Hq] slopes (metal_flash_attn/_kernel.py:1275-1285).
+
+    Returns (contiguous fp32 slopes on `device`, batch stride) with batch
+    stride 0 for per-head slopes and Hq for per-(batch, head) slopes, so no
+    [B*Hq] broadcast copy is made.
+    """
+    if alibi_slopes is None:
+        return None, 0
+    s = alibi_slopes
+    if s.dim() == 1 and s.shape[0] == Hq:
+        bstride = 0
+    elif s.dim() == 2 and tuple(s.shape) == (B, Hq):
+        bstride = Hq
+    else:
+        raise ValueError(
+            f"mtlflashattn_amd: alibi_slopes must be [Hq={Hq}] or [B={B}, Hq={Hq}], got {tuple(s.shape)}"
+        )
+    return s.to(device=device, dtype=torch.float32).contiguous(), bstride
+
+
+def _check_device(*tensors):
+    for t in tensors:
+        if t.device.type != "cuda" or torch.version.hip is None:
+            raise NotImplementedError(
+                f"mtlflashattn_amd: device {t.device.type!r} not supported (ROCm GPU only)"
+            )
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"mtlflashattn_amd: tensors on different devices ({dev} vs {t.device})")
+
+
+def _fits_abi(x: torch.Tensor) -> bool:
+    """16-byte aligned base and 16-byte multiple strides (size-1 dims ignored)."""
+    if x.stride(-1) != 1 and x.shape[-1] > 1:
+        return False
+    if x.data_ptr() % 16:
+        return False
+    al = 16 // x.element_size()
+    return all(st % al == 0 for st, n in zip(x.stride()[:-1], x.shape[:-1]) if n > 1)
+
+
+def _strides_bsh(x: torch.Tensor):
+    """(batch, seq, head) element strides of a [B, S, H, D] view; 0 for size-1 dims."""
+    return tuple(int(st) if n > 1 else 0 for st, n in zip(x.stride()[:3], x.shape[:3]))
+
+
+def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, alibi, alibi_bstride,
+         cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None):
+    """Launch the HIP forward on [B, S, H, D] views q, k, v and write `out`.
+
+    out: [B, Sq, Hq, D] tensor of q.dtype or float32 (full-precision output).
+    Varlen: q/k/v/out are [1, total, H, D] views, cu_q/cu_k int32 device
+    tensors, seqlen_q/seqlen_k the maximum per-sequence lengths.
+    """
+    _kernel_mode()
+    B, Sq, Hq, D = q.shape
+    Hkv = k.shape[2]
+    varlen = cu_q is not None
+    batch = (cu_q.shape[0] - 1) if varlen else B
+    Lq = int(seqlen_q) if varlen else Sq
+    Lk = int(seqlen_k) if varlen else k.shape[1]
+    if batch == 0 or Lq == 0 or Hq == 0 or out.numel() == 0:
+        return out
+    if k.shape[1] == 0 or Lk == 0:
+        return out.zero_()  # no keys: every row is fully masked -> 0
+
+    Dp = -(-D // 8) * 8
+    if Dp != D:  # the kernels read 16-byte chunks: zero-pad the head dim
+        q, k, v = (F.pad(t, (0, Dp - D)) for t in (q, k, v))
+    q, k, v = (t if _fits_abi(t) else t.contiguous() for t in (q, k, v))
+    dst = out
+    if Dp != D or not _fits_abi(out) or out.stride(-1) != 1:
+        dst = torch.empty(out.shape[:-1] + (Dp,), dtype=out.dtype, device=out.device)
+
+    p = _hip.MfaFwdParams()
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), dst.data_ptr()
+    p.q_batch_stride, p.q_seq_stride, p.q_head_stride = _strides_bsh(q)
+    p.k_batch_stride, p.k_seq_stride, p.k_head_stride = _strides_bsh(k)
+    p.v_batch_stride, p.v_seq_stride, p.v_head_stride = _strides_bsh(v)
+    p.o_batch_stride, p.o_seq_stride, p.o_head_stride = _strides_bsh(dst)
+    p.batch, p.heads_q, p.heads_kv = batch, Hq, Hkv
+    p.seqlen_q, p.seqlen_k, p.head_dim = Lq, Lk, Dp
+    if varlen:
+        p.cu_seqlens_q, p.cu_seqlens_k = cu_q.data_ptr(), cu_k.data_ptr()
+    p.scale = float(scale)
+    p.softcap = float(softcap)
+    p.window_left, p.window_right = int(window_left), int(window_right)
+    p.causal = 1 if causal else 0
+    if alibi is not None:
+        p.alibi_slopes = alibi.data_ptr()
+        p.alibi_batch_stride = alibi_bstride
+    p.dtype_in = _hip.DTYPE_CODES[q.dtype]
+    p.dtype_out = _hip.DTYPE_CODES[out.dtype]
+    with torch.cuda.device(q.device):
+        _hip.fwd(p, torch.cuda.current_stream(q.device).cuda_stream)
+    if dst is not out:
+        out.copy_(dst[..., :D])
+    return out
+
+
+def _out_dtype(q, out_dtype):
+    if out_dtype is None or out_dtype == q.dtype:
+        return q.dtype
+    if out_dtype != torch.float32:
+        raise ValueError(f"mtlflashattn_amd: out_dtype must be None, q.dtype or torch.float32, got {out_dtype}")
+    return torch.float32
+
+
+def flash_attn_forward(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1,
+                       alibi_slopes=None, out_dtype=None):
+    """q: [B,Hq,Lq,D], k/v: [B,Hkv,Lk,D] (heads-second, any strides).
+
+    Returns [B,Hq,Lq,D] contiguous, in q.dtype (metal_flash_attn/_kernel.py:1052-1056).
+    out_dtype=torch.float32 returns the kernel's fp32 result before the
+    final rounding to q.dtype (the parity mode for bf16/fp16 inputs).
+    """
+    if _trace_enabled():
+        _record_trace(q.dtype, q.shape[-1], q.shape[2], k.shape[2], causal)
+    if softcap < 0:
+        # _kernel.py:1070-1073: reject here so direct callers cannot diverge
+        raise ValueError("mtlflashattn_amd: softcap must be >= 0 (0 disables capping)")
+    B, Hq, Lq, D = q.shape
+    Hkv = k.shape[1]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
+    alibi, bstride = _alibi_arg(alibi_slopes, B, Hq, q.device)
+    _check_device(q, k, v)
+    if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise NotImplementedError(f"mtlflashattn_amd: dtype {q.dtype} (q/k/v must match, fp16/bf16/fp32)")
+    if D > MAX_HEAD_DIM:
+        raise NotImplementedError(f"mtlflashattn_amd: head_dim {D} > {MAX_HEAD_DIM}")
+    out = torch.empty(B, Hq, Lq, D, dtype=_out_dtype(q, out_dtype), device=q.device)
+    _run(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2),
+         scale=scale, causal=causal, softcap=softcap, window_left=window_left,
+         window_right=window_right, alibi=alibi, alibi_bstride=bstride)
+    return out
+
+
+def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1,
+                 alibi_slopes=None, out_dtype=None):
+    """Heads-third forward: q [B,Lq,Hq,D], k/v [B,Lk,Hkv,D] -> [B,Lq,Hq,D].
+
+    Same result as flash_attn_forward on the transposed views followed by
+    `.transpose(1, 2).contiguous()` (metal_flash_attn/__init__.py:93-99), but
+    the kernel writes the heads-third output directly (no layout copies).
+    """
+    if _trace_enabled():
+        _record_trace(q.dtype, q.shape[-1], q.shape[1], k.shape[1], causal)
+    if softcap < 0:
+        raise ValueError("mtlflashattn_amd: softcap must be >= 0 (0 disables capping)")
+    B, Lq, Hq, D = q.shape
+    alibi, bstride = _alibi_arg(alibi_slopes, B, Hq, q.device)
+    out = torch.empty(B, Lq, Hq, D, dtype=_out_dtype(q, out_dtype), device=q.device)
+    return _run(q, k, v, out, scale=scale, causal=causal, softcap=softcap, window_left=window_left,
+                window_right=window_right, alibi=alibi, alibi_bstride=bstride)
+
+
+def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0, window_left=-1,
+                   window_right=-1, alibi_slopes=None, out_dtype=None):
+    """Packed varlen forward in ONE launch: q [Tq,Hq,D], k/v [Tk,Hkv,D].
+
+    cu_q/cu_k: int32 [batch+1] device tensors; max_q/max_k: the longest
+    sequence lengths.  Replaces the reference's per-sequence loop of B=1
+    dispatches (metal_flash_attn/__init__.py:165-182) with the same result.
+    """
+    batch = cu_q.shape[0] - 1
+    Hq = q.shape[1]
+    if alibi_slopes is not None and alibi_slopes.dim() == 2 and tuple(alibi_slopes.shape) != (batch, Hq):
+        raise ValueError(
+            f"mtlflashattn_amd: alibi_slopes must be [Hq={Hq}] or [B={batch}, Hq={Hq}], "
+            f"got {tuple(alibi_slopes.shape)}"
+        )
+    alibi, bstride = _alibi_arg(alibi_slopes, batch, Hq, q.device)
+    if _trace_enabled():
+        _record_trace(q.dtype, q.shape[-1], max_q, max_k, causal, "hip-varlen")
+    out = torch.empty(q.shape, dtype=_out_dtype(q, out_dtype), device=q.device)
+    cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
+    cu_k = cu_k.to(device=q.device, dtype=torch.int32).contiguous()
+    return _run(q[None], k[None], v[None], out[None], scale=scale, causal=causal, softcap=softcap,
+                window_left=window_left, window_right=window_right, alibi=alibi, alibi_bstride=bstride,
+                cu_q=cu_q, cu_k=cu_k, seqlen_q=max_q, seqlen_k=max_k)[0]
+
+
+def launch_info(q, k, v, causal=False, softcap=0.0, alibi=False, window_left=-1, window_right=-1):
+    """Kernel geometry (name, grid, tile) for heads-third q/k/v; no launch."""
+    B, Lq, Hq, D = q.shape
+    p = _hip.MfaFwdParams()
+    p.q = p.k = p.v = p.o = 256  # placeholder aligned addresses: nothing is read
+    p.q_batch_stride, p.q_seq_stride, p.q_head_stride = Lq * Hq * D, Hq * D, D
+    p.k_batch_stride, p.k_seq_stride, p.k_head_stride = k.shape[1] * k.shape[2] * D, k.shape[2] * D, D
+    p.v_batch_stride, p.v_seq_stride, p.v_head_stride = p.k_batch_stride, p.k_seq_stride, p.k_head_stride
+    p.o_batch_stride, p.o_seq_stride, p.o_head_stride = p.q_batch_stride, p.q_seq_stride, p.q_head_stride
+    p.batch, p.heads_q, p.heads_kv = B, Hq, k.shape[2]
+    p.seqlen_q, p.seqlen_k, p.head_dim = Lq, k.shape[1], -(-D // 8) * 8
+    p.scale = 1.0
+    p.softcap = float(softcap)
+    p.window_left, p.window_right, p.causal = window_left, window_right, int(causal)
+    p.alibi_slopes = 256 if alibi else None
+    p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
+    return _hip.launch_info(p)

@@ -1,0 +1,894 @@
+// mfa_fwd.hip -- MI355X (gfx950 / CDNA4) flash-attention forward kernels and
+// the C ABI declared in include/mfa.h.
+//
+// Reference semantics: metal_flash_attn/_kernel.py:32-87 (the scalar v0 kernel
+// states the mask/bias/online-softmax math most plainly) and :1165-1208 (the
+// chunked fp32 torch path, whose results these kernels must reproduce).
+//
+// Design (one kernel family, FA-2 forward, one workgroup = 4 wavefronts):
+//  * The score tile is computed TRANSPOSED, S^T = K * Q^T, with
+//    v_mfma_f32_32x32x16_{bf16,f16} (fp32 inputs: v_mfma_f32_32x32x2_f32).
+//    In the 32x32 MFMA accumulator layout lane l holds column l%32, so every
+//    lane owns exactly one query row: max/sum/rescale are lane-local and the
+//    only cross-lane step per K/V block is one v_permlane32_swap to merge the
+//    two half-waves that share a query.
+//  * O is accumulated transposed as well, O^T = V^T * P^T, whose accumulator
+//    again gives each lane one query, so the online-softmax rescale of O is a
+//    lane-local multiply.  P^T is fed to the MFMA straight from the S^T
+//    accumulator registers (converted to bf16/f16 in registers); it never
+//    touches LDS.  The k-slot order of that MFMA follows the accumulator
+//    row order, and V^T is written to LDS in the same (bit-permuted) key
+//    order so that each lane still reads 16 contiguous bytes.
+//  * Q is staged through LDS once (coalesced global reads) and then lives in
+//    registers as the MFMA B operand.  K and V stream through two LDS buffers:
+//    the global loads of block j+1 are issued before the MFMAs of block j and
+//    written to the other buffer after them, one barrier per block.
+//  * Keys outside [lo(q), hi(q)] (bottom-right causal, sliding window, the
+//    sequence end) are skipped a whole block at a time where a block is
+//    entirely outside the range of every query of the workgroup, masked
+//    element-wise only on the boundary blocks of each wavefront, and
+//    untouched elsewhere.
+//  * O and l are rescaled only in blocks where some row's running max grew
+//    (a wave-uniform branch); the running max itself is always exact, so the
+//    largest probability of a row is exactly 1.0 and loses nothing when P is
+//    rounded to 16 bits for the PV MFMA.
+//  * Workgroups are ordered heaviest-tile-first (causal: last query tile
+//    first) and, where the number of K/V head groups is a multiple of 8,
+//    all tiles of one K/V head are placed on one XCD so its K/V stays in that
+//    XCD's L2.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <type_traits>
+
+#include "mfa.h"
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Kernel argument block (copied by value into the kernarg segment).
+struct KArgs {
+    const char* q;
+    const char* k;
+    const char* v;
+    char* o;
+    // element strides
+    int64_t qb, qs, qh;
+    int64_t kb, ks, kh;
+    int64_t vb, vs, vh;
+    int64_t ob, os, oh;
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    const float* alibi;
+    int32_t alibi_bstride;
+    int32_t B, Hq, Hkv, Lq, Lk, D;
+    float scale;      // softmax scale
+    float scale_log2; // scale * log2(e)
+    float softcap;    // 0 = off
+    float softcap_k;  // 2 * log2(e) / softcap
+    int32_t wl, wr, causal;
+    int32_t out_f32;
+    // schedule
+    int32_t T;        // query tiles per (sequence, head)
+    int32_t U;        // (sequence, head) units = B * Hq
+    int32_t upx;      // units per XCD (grouped schedule)
+    int32_t grouped;  // 1: XCD-grouped by K/V head, 0: linear
+};
+
+// ----------------------------------------------------------------------------
+// small device helpers
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// value of `x` in lane (lane ^ 32) and in this lane, combined by max
+__device__ __forceinline__ float max_halves(float x) {
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float(sw[0]) + __int_as_float(sw[1]);
+}
+
+// Accumulator row of register r in the 32x32 MFMA C layout, minus the
+// half-wave term 4*(lane/32): rows 8*(r/4) + r%4.
+__device__ __forceinline__ constexpr int acc_row(int r) { return 8 * (r >> 2) + (r & 3); }
+
+// Position of key kk (0..31 inside a 32-key group) in the V^T LDS rows:
+// bits 2 and 3 swapped, so that the 8 keys one half-wave feeds to one
+// PV MFMA (accumulator registers 8*st..8*st+7) are contiguous.
+__device__ __forceinline__ int vt_pos(int kk) {
+    return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+}
+
+// Map the linear workgroup id to (sequence, q head, query tile).
+// Returns false for padding workgroups.
+__device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int& hq, int& t) {
+    int unit, tt;
+    if (a.grouped) {
+        // workgroup ids are dealt round-robin over the 8 XCDs; XCD x owns the
+        // K/V head groups g = b*Hkv + hkv with g % 8 == x, all their q heads
+        // and all their tiles.
+        const int xcd = bid & 7;
+        const int slot = bid >> 3;
+        tt = slot / a.upx;
+        const int j = slot - tt * a.upx;
+        const int R = a.Hq / a.Hkv;
+        const int jg = j / R;
+        const int g = xcd + 8 * jg;
+        const int r = j - jg * R;
+        b = g / a.Hkv;
+        const int hkv = g - b * a.Hkv;
+        hq = hkv * R + r;
+        unit = b * a.Hq + hq;
+        if (unit >= a.U) return false;
+    } else {
+        tt = bid / a.U;
+        unit = bid - tt * a.U;
+        b = unit / a.Hq;
+        hq = unit - b * a.Hq;
+    }
+    t = a.T - 1 - tt;  // heaviest (last) query tiles first
+    return t >= 0;
+}
+
+struct SeqView {
+    const char* q;
+    const char* k;
+    const char* v;
+    char* o;
+    int Lq, Lk;
+};
+
+// ES: input element bytes; the output element size follows a.out_f32.
+template <int ES>
+__device__ __forceinline__ SeqView seq_view(const KArgs& a, int b, int hq) {
+    SeqView s;
+    const int OES = a.out_f32 ? 4 : ES;
+    const int hkv = hq / (a.Hq / a.Hkv);  // grouped-query mapping (_kernel.py:54)
+    int64_t qo, ko;
+    if (a.cu_q) {
+        const int q_start = a.cu_q[b];
+        const int k_start = a.cu_k[b];
+        s.Lq = a.cu_q[b + 1] - q_start;
+        s.Lk = a.cu_k[b + 1] - k_start;
+        qo = (int64_t)q_start * a.qs;
+        ko = (int64_t)k_start;
+        s.q = a.q + (qo + (int64_t)hq * a.qh) * ES;
+        s.k = a.k + (ko * a.ks + (int64_t)hkv * a.kh) * ES;
+        s.v = a.v + (ko * a.vs + (int64_t)hkv * a.vh) * ES;
+        s.o = a.o + ((int64_t)q_start * a.os + (int64_t)hq * a.oh) * OES;
+    } else {
+        s.Lq = a.Lq;
+        s.Lk = a.Lk;
+        s.q = a.q + ((int64_t)b * a.qb + (int64_t)hq * a.qh) * ES;
+        s.k = a.k + ((int64_t)b * a.kb + (int64_t)hkv * a.kh) * ES;
+        s.v = a.v + ((int64_t)b * a.vb + (int64_t)hkv * a.vh) * ES;
+        s.o = a.o + ((int64_t)b * a.ob + (int64_t)hq * a.oh) * OES;
+    }
+    return s;
+}
+
+// Valid key interval [lo, hi] of the query with bottom-right center `c`
+// (_kernel.py:56-64).  Window bounds are clamped on the host so c+wr cannot
+// overflow.
+__device__ __forceinline__ int key_lo(const KArgs& a, int c) { return a.wl >= 0 ? max(c - a.wl, 0) : 0; }
+__device__ __forceinline__ int key_hi(const KArgs& a, int c, int Lk) {
+    int hi = Lk - 1;
+    if (a.causal) hi = min(hi, c);
+    if (a.wr >= 0) hi = min(hi, c + a.wr);
+    return hi;
+}
+
+// ----------------------------------------------------------------------------
+// Online softmax over one K/V block of S^T accumulators (shared by the 16-bit
+// and fp32 kernels, which use the same 32x32 accumulator layout).
+//
+// s[qb][kb][r]: raw score of query (32*qb + lane%32) and key
+//   j + 32*kb + 4*(lane/32) + acc_row(r).
+// On return s holds the (unnormalised) probabilities p.
+template <int QB, int NKB, int DB, bool BIAS>
+__device__ __forceinline__ void softmax_block(const KArgs& a, f32x16_t (&s)[QB][NKB], f32x16_t (&o)[DB][QB],
+                                              float (&m_run)[QB], float (&l_part)[QB], const int (&center)[QB],
+                                              const int (&lo)[QB], const int (&hi)[QB], const float (&slope)[QB],
+                                              int j, int half, bool masked) {
+    if constexpr (BIAS) {
+        // natural-log units: x = scale*s, soft-cap, ALiBi (_kernel.py:75-77)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[qb][kb][r] *= a.scale;
+        if (a.softcap > 0.f) {
+            // c * tanh(x / c) = c - 2c / (exp(2x/c) + 1)
+            const float c2 = -2.f * a.softcap;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float e = fast_exp2(s[qb][kb][r] * a.softcap_k);
+                        s[qb][kb][r] = fmaf(c2, __builtin_amdgcn_rcpf(e + 1.f), a.softcap);
+                    }
+        }
+        if (a.alibi) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    const float cf = (float)(center[qb] - (j + 32 * kb + 4 * half));
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        s[qb][kb][r] = fmaf(-slope[qb], fabsf(cf - (float)acc_row(r)), s[qb][kb][r]);
+                }
+        }
+    }
+    if (masked) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                const int kbase = j + 32 * kb + 4 * half;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbase + acc_row(r);
+                    const bool ok = (key >= lo[qb]) & (key <= hi[qb]);
+                    s[qb][kb][r] = ok ? s[qb][kb][r] : -INFINITY;
+                }
+            }
+    }
+    const float c = BIAS ? kLog2e : a.scale_log2;
+    float mx[QB];
+    bool need = false;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        float m = s[qb][0][0];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) m = fmaxf(m, s[qb][kb][r]);
+        mx[qb] = max_halves(m);
+        need |= mx[qb] > m_run[qb];
+    }
+    if (__any(need)) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const float mn = fmaxf(m_run[qb], mx[qb]);
+            const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2((m_run[qb] - mn) * c);
+            m_run[qb] = mn;
+            l_part[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][qb][r] *= alpha;
+        }
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const float mu = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb] * c;
+        float acc = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(fmaf(s[qb][kb][r], c, -mu));
+                s[qb][kb][r] = p;
+                acc += p;
+            }
+        l_part[qb] += acc;
+    }
+}
+
+// Normalise and store O^T accumulators: lane (half, q) holds
+// d = 32*db + 8*g + 4*half + {0..3} for g = 0..3.
+template <int QB, int DB, bool IS_BF16>
+__device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32x16_t (&o)[DB][QB],
+                                          const float (&l_part)[QB], int qrow0, int lane) {
+    const int l32 = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const float l = sum_halves(l_part[qb]);
+        const float inv = l > 0.f ? 1.f / l : 0.f;  // fully masked rows -> 0 (_kernel.py:85)
+        const int qrow = qrow0 + 32 * qb + l32;
+        if (qrow >= sv.Lq) continue;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * half;
+                if (d >= a.D) continue;
+                const float v0 = o[db][qb][4 * g + 0] * inv, v1 = o[db][qb][4 * g + 1] * inv;
+                const float v2 = o[db][qb][4 * g + 2] * inv, v3 = o[db][qb][4 * g + 3] * inv;
+                if (a.out_f32) {
+                    float* dst = reinterpret_cast<float*>(sv.o) + (int64_t)qrow * a.os + d;
+                    *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+                } else if constexpr (IS_BF16) {
+                    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+                    bf16x4_t w = {(__bf16)v0, (__bf16)v1, (__bf16)v2, (__bf16)v3};
+                    *reinterpret_cast<bf16x4_t*>(reinterpret_cast<__bf16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+                } else {
+                    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
+                    f16x4_t w = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+                    *reinterpret_cast<f16x4_t*>(reinterpret_cast<_Float16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+                }
+            }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// 16-bit (bf16 / fp16) kernel.
+//   DP  : head dim padded to a multiple of 32 (32, 64, 96, 128)
+//   QB  : 32-query column blocks per wavefront (workgroup rows = 4*32*QB)
+//   NKB : 32-key row blocks per K/V block (keys per block = 32*NKB)
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
+__global__ void __launch_bounds__(kThreads) mfa_fwd16_kernel(KArgs a) {
+    constexpr int BM = kWaves * QB * 32;
+    constexpr int BN = NKB * 32;
+    constexpr int DS = DP / 16;  // QK^T k-steps
+    constexpr int DB = DP / 32;  // O^T row blocks
+    constexpr int KST = DP + 8;  // K / Q LDS row stride (elements): +16 B against bank conflicts
+    constexpr int VST = BN + 8;  // V^T LDS row stride (elements)
+    constexpr int K_ELEMS = BN * KST;
+    constexpr int V_ELEMS = DP * VST;
+    constexpr int KV_ELEMS = 2 * (K_ELEMS + V_ELEMS);
+    constexpr int Q_ELEMS = BM * KST;
+    constexpr int SMEM = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+    constexpr int CPR = DP / 8;                          // 16-byte chunks per row
+    constexpr int KCH = (BN * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
+    typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
+
+    __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
+
+    int b, hq, tile;
+    if (!decode_tile(a, blockIdx.x, b, hq, tile)) return;
+    const SeqView sv = seq_view<2>(a, b, hq);
+    const int q0 = tile * BM;
+    if (q0 >= sv.Lq) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
+    const int dq = Lk - Lq;
+
+    // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
+    for (int c = tid; c < BM * CPR; c += kThreads) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        u32x4_t val = {0, 0, 0, 0};
+        if (q0 + row < Lq && col < D)
+            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 2);
+        *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
+    }
+    __syncthreads();
+    const int wq0 = q0 + wave * QB * 32;  // first query row of this wavefront
+    op_t qf[QB][DS];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int s = 0; s < DS; ++s)
+            qf[qb][s] = *reinterpret_cast<const op_t*>(smem + (wave * QB * 32 + qb * 32 + l32) * KST + 16 * s + 8 * half);
+    __syncthreads();
+
+    // ---- per-lane query state
+    int center[QB], lo[QB], hi[QB];
+    float slope[QB], m_run[QB], l_part[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        center[qb] = wq0 + 32 * qb + l32 + dq;
+        lo[qb] = key_lo(a, center[qb]);
+        hi[qb] = key_hi(a, center[qb], Lk);
+        slope[qb] = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+        m_run[qb] = -INFINITY;
+        l_part[qb] = 0.f;
+    }
+    f32x16_t o[DB][QB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][qb][r] = 0.f;
+
+    // ---- key range of the workgroup and of this wavefront
+    const int qlast = min(q0 + BM, Lq) - 1;
+    const int klo = key_lo(a, q0 + dq);
+    const int khi = key_hi(a, qlast + dq, Lk);
+    const int jbeg = (klo / BN) * BN;
+    const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
+    const int wlast = min(wq0 + QB * 32, Lq) - 1;  // < wq0 when the wave has no rows
+    const bool wave_live = wlast >= wq0;
+    const int w_lo_first = key_lo(a, wq0 + dq), w_lo_last = key_lo(a, wlast + dq);
+    const int w_hi_first = key_hi(a, wq0 + dq, Lk), w_hi_last = key_hi(a, wlast + dq, Lk);
+
+    // ---- K/V streaming: global -> registers (block j+1) -> LDS buffer
+    u32x4_t kreg[KCH], vreg[KCH];
+    auto gload = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + kThreads * i;
+            const int row = c / CPR, col = (c % CPR) * 8;
+            const bool ok = (c < BN * CPR) && (j + row < Lk) && (col < D);
+            u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+            if (ok) {
+                kv = *reinterpret_cast<const u32x4_t*>(sv.k + ((int64_t)(j + row) * a.ks + col) * 2);
+                vv = *reinterpret_cast<const u32x4_t*>(sv.v + ((int64_t)(j + row) * a.vs + col) * 2);
+            }
+            kreg[i] = kv;
+            vreg[i] = vv;
+        }
+    };
+    auto swrite = [&](int buf) {
+        uint16_t* kbuf = smem + buf * K_ELEMS;
+        uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + kThreads * i;
+            if (c < BN * CPR) {
+                const int row = c / CPR, col = (c % CPR) * 8;
+                *reinterpret_cast<u32x4_t*>(kbuf + row * KST + col) = kreg[i];
+                const int p = (row & ~31) + vt_pos(row & 31);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t w = vreg[i][e];
+                    vtb[(col + 2 * e) * VST + p] = (uint16_t)(w & 0xffffu);
+                    vtb[(col + 2 * e + 1) * VST + p] = (uint16_t)(w >> 16);
+                }
+            }
+        }
+    };
+
+    if (nblk > 0) {
+        gload(jbeg);
+        swrite(0);
+    }
+    for (int it = 0; it < nblk; ++it) {
+        const int j = jbeg + it * BN;
+        const int buf = it & 1;
+        const bool more = it + 1 < nblk;
+        if (more) gload(j + BN);
+        __syncthreads();
+
+        const bool skip = !wave_live || (j + BN - 1 < w_lo_first) || (j > w_hi_last);
+        if (!skip) {
+            const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
+            const uint16_t* kbuf = smem + buf * K_ELEMS;
+            const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;
+            // S^T = K Q^T
+            f32x16_t sacc[QB][NKB];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sacc[qb][kb][r] = 0.f;
+#pragma unroll
+                for (int s = 0; s < DS; ++s) {
+                    const op_t kf = *reinterpret_cast<const op_t*>(kbuf + (32 * kb + l32) * KST + 16 * s + 8 * half);
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) {
+                        if constexpr (IS_BF16)
+                            sacc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][s], sacc[qb][kb], 0, 0, 0);
+                        else
+                            sacc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qb][s], sacc[qb][kb], 0, 0, 0);
+                    }
+                }
+            }
+            softmax_block<QB, NKB, DB, BIAS>(a, sacc, o, m_run, l_part, center, lo, hi, slope, j, half, masked);
+            // P^T as MFMA B operands, straight from the accumulators
+            op_t pf[QB][NKB][2];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int st = 0; st < 2; ++st)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            if constexpr (IS_BF16)
+                                pf[qb][kb][st][i] = (__bf16)sacc[qb][kb][8 * st + i];
+                            else
+                                pf[qb][kb][st][i] = (_Float16)sacc[qb][kb][8 * st + i];
+                        }
+            // O^T += V^T P^T
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int st = 0; st < 2; ++st) {
+                        const op_t vf = *reinterpret_cast<const op_t*>(vtb + (32 * db + l32) * VST + 32 * kb + 16 * st + 8 * half);
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb) {
+                            if constexpr (IS_BF16)
+                                o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][kb][st], o[db][qb], 0, 0, 0);
+                            else
+                                o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[qb][kb][st], o[db][qb], 0, 0, 0);
+                        }
+                    }
+        }
+        if (more) swrite(buf ^ 1);
+    }
+
+    store_out<QB, DB, IS_BF16>(a, sv, o, l_part, wq0, lane);
+}
+
+// ----------------------------------------------------------------------------
+// fp32 kernel: same structure with v_mfma_f32_32x32x2_f32.  K-slot layout of
+// the 32x32x2 MFMA: lane (half, x) supplies k = half, so QK^T step s uses
+// d = s + half*DP/2 and PV step r uses the key held in accumulator register r.
+template <int DP, int NKB, bool BIAS>
+__global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
+    constexpr int QB = 1;
+    constexpr int BM = kWaves * 32;
+    constexpr int BN = NKB * 32;
+    constexpr int DH = DP / 2;   // d values per half-wave
+    constexpr int DB = DP / 32;
+    constexpr int KST = DP + 4;  // K / Q row stride (floats)
+    constexpr int VST = DP + 8;  // V row stride (floats): the half-waves read rows 4 apart
+    constexpr int K_ELEMS = BN * KST;
+    constexpr int V_ELEMS = BN * VST;
+    constexpr int KV_ELEMS = 2 * (K_ELEMS + V_ELEMS);
+    constexpr int Q_ELEMS = BM * KST;
+    constexpr int SMEM = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+    constexpr int CPR = DP / 4;
+    constexpr int KCH = (BN * CPR + kThreads - 1) / kThreads;
+
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+
+    int b, hq, tile;
+    if (!decode_tile(a, blockIdx.x, b, hq, tile)) return;
+    const SeqView sv = seq_view<4>(a, b, hq);
+    const int q0 = tile * BM;
+    if (q0 >= sv.Lq) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
+    const int dq = Lk - Lq;
+
+    for (int c = tid; c < BM * CPR; c += kThreads) {
+        const int row = c / CPR, col = (c % CPR) * 4;
+        u32x4_t val = {0, 0, 0, 0};
+        if (q0 + row < Lq && col < D)
+            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 4);
+        *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
+    }
+    __syncthreads();
+    const int wq0 = q0 + wave * 32;
+    float qf[DH];
+#pragma unroll
+    for (int s = 0; s < DH; s += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(smem + (wave * 32 + l32) * KST + half * DH + s);
+        qf[s] = t.x;
+        qf[s + 1] = t.y;
+        qf[s + 2] = t.z;
+        qf[s + 3] = t.w;
+    }
+    __syncthreads();
+
+    int center[QB], lo[QB], hi[QB];
+    float slope[QB], m_run[QB], l_part[QB];
+    center[0] = wq0 + l32 + dq;
+    lo[0] = key_lo(a, center[0]);
+    hi[0] = key_hi(a, center[0], Lk);
+    slope[0] = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+    m_run[0] = -INFINITY;
+    l_part[0] = 0.f;
+    f32x16_t o[DB][QB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][0][r] = 0.f;
+
+    const int qlast = min(q0 + BM, Lq) - 1;
+    const int klo = key_lo(a, q0 + dq);
+    const int khi = key_hi(a, qlast + dq, Lk);
+    const int jbeg = (klo / BN) * BN;
+    const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
+    const int wlast = min(wq0 + 32, Lq) - 1;
+    const bool wave_live = wlast >= wq0;
+    const int w_lo_first = key_lo(a, wq0 + dq), w_lo_last = key_lo(a, wlast + dq);
+    const int w_hi_first = key_hi(a, wq0 + dq, Lk), w_hi_last = key_hi(a, wlast + dq, Lk);
+
+    u32x4_t kreg[KCH], vreg[KCH];
+    auto gload = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + kThreads * i;
+            const int row = c / CPR, col = (c % CPR) * 4;
+            const bool ok = (c < BN * CPR) && (j + row < Lk) && (col < D);
+            u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+            if (ok) {
+                kv = *reinterpret_cast<const u32x4_t*>(sv.k + ((int64_t)(j + row) * a.ks + col) * 4);
+                vv = *reinterpret_cast<const u32x4_t*>(sv.v + ((int64_t)(j + row) * a.vs + col) * 4);
+            }
+            kreg[i] = kv;
+            vreg[i] = vv;
+        }
+    };
+    auto swrite = [&](int buf) {
+        float* kbuf = smem + buf * K_ELEMS;
+        float* vbuf = smem + 2 * K_ELEMS + buf * V_ELEMS;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + kThreads * i;
+            if (c < BN * CPR) {
+                const int row = c / CPR, col = (c % CPR) * 4;
+                *reinterpret_cast<u32x4_t*>(kbuf + row * KST + col) = kreg[i];
+                *reinterpret_cast<u32x4_t*>(vbuf + row * VST + col) = vreg[i];
+            }
+        }
+    };
+
+    if (nblk > 0) {
+        gload(jbeg);
+        swrite(0);
+    }
+    for (int it = 0; it < nblk; ++it) {
+        const int j = jbeg + it * BN;
+        const int buf = it & 1;
+        const bool more = it + 1 < nblk;
+        if (more) gload(j + BN);
+        __syncthreads();
+
+        const bool skip = !wave_live || (j + BN - 1 < w_lo_first) || (j > w_hi_last);
+        if (!skip) {
+            const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
+            const float* kbuf = smem + buf * K_ELEMS;
+            const float* vbuf = smem + 2 * K_ELEMS + buf * V_ELEMS;
+            f32x16_t sacc[QB][NKB];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[0][kb][r] = 0.f;
+#pragma unroll
+                for (int s = 0; s < DH; s += 4) {
+                    const float4 kf = *reinterpret_cast<const float4*>(kbuf + (32 * kb + l32) * KST + half * DH + s);
+                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[s], sacc[0][kb], 0, 0, 0);
+                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[s + 1], sacc[0][kb], 0, 0, 0);
+                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[s + 2], sacc[0][kb], 0, 0, 0);
+                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[s + 3], sacc[0][kb], 0, 0, 0);
+                }
+            }
+            softmax_block<QB, NKB, DB, BIAS>(a, sacc, o, m_run, l_part, center, lo, hi, slope, j, half, masked);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float vf = vbuf[(32 * kb + 4 * half + acc_row(r)) * VST + 32 * db + l32];
+                        o[db][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf, sacc[0][kb][r], o[db][0], 0, 0, 0);
+                    }
+        }
+        if (more) swrite(buf ^ 1);
+    }
+
+    // fp32 output (out_f32 is implied for fp32 input)
+    store_out<QB, DB, true>(a, sv, o, l_part, wq0, lane);
+}
+
+// ----------------------------------------------------------------------------
+// host side
+
+thread_local char g_err[512] = "";
+
+int set_err(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+typedef void (*kernel_fn)(KArgs);
+
+struct KernelCfg {
+    kernel_fn fn;
+    int rows;  // query rows per workgroup
+    int keys;  // keys per K/V block
+    int lds;   // LDS bytes
+    const char* name;
+};
+
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
+KernelCfg cfg16(const char* name) {
+    constexpr int BM = kWaves * QB * 32, BN = NKB * 32;
+    constexpr int kv = 2 * (BN * (DP + 8) + DP * (BN + 8)), qs = BM * (DP + 8);
+    return KernelCfg{mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs), name};
+}
+template <int DP, int NKB, bool BIAS>
+KernelCfg cfg32(const char* name) {
+    constexpr int BM = kWaves * 32, BN = NKB * 32;
+    constexpr int kv = 2 * (BN * (DP + 4) + BN * (DP + 8)), qs = BM * (DP + 4);
+    return KernelCfg{mfa_fwd32_kernel<DP, NKB, BIAS>, BM, BN, 4 * (kv > qs ? kv : qs), name};
+}
+
+// tile configuration per (dtype, padded head dim, bias)
+template <bool IS_BF16, bool BIAS>
+KernelCfg select16(int dp) {
+    switch (dp) {
+        case 32: return cfg16<32, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32,q64,k64>" : "mfa_fwd16<f16,d32,q64,k64>");
+        case 64: return cfg16<64, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64,q64,k64>" : "mfa_fwd16<f16,d64,q64,k64>");
+        case 96: return cfg16<96, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d96,q32,k64>" : "mfa_fwd16<f16,d96,q32,k64>");
+        default: return cfg16<128, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d128,q32,k64>" : "mfa_fwd16<f16,d128,q32,k64>");
+    }
+}
+template <bool BIAS>
+KernelCfg select32(int dp) {
+    switch (dp) {
+        case 32: return cfg32<32, 1, BIAS>("mfa_fwd32<f32,d32,q32,k32>");
+        case 64: return cfg32<64, 1, BIAS>("mfa_fwd32<f32,d64,q32,k32>");
+        case 96: return cfg32<96, 1, BIAS>("mfa_fwd32<f32,d96,q32,k32>");
+        default: return cfg32<128, 1, BIAS>("mfa_fwd32<f32,d128,q32,k32>");
+    }
+}
+
+struct Plan {
+    KernelCfg cfg;
+    KArgs args;
+    int grid;
+    bool empty;
+};
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int make_plan(const mfa_fwd_params* p, Plan* plan) {
+    if (!p) return set_err(MFA_ERR_INVALID, "mfa_fwd: params is NULL");
+    const int din = p->dtype_in, dout = p->dtype_out;
+    if (din != MFA_DTYPE_F16 && din != MFA_DTYPE_BF16 && din != MFA_DTYPE_F32)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: unknown dtype_in %d", din);
+    if (dout != din && dout != MFA_DTYPE_F32)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: dtype_out %d must equal dtype_in %d or be fp32", dout, din);
+    const int D = p->head_dim;
+    if (D <= 0 || D > MFA_MAX_HEAD_DIM)
+        return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: head_dim %d outside [1, %d]", D, MFA_MAX_HEAD_DIM);
+    if (D % 8 != 0)
+        return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: head_dim %d is not a multiple of 8 (pad it)", D);
+    if (p->batch < 0 || p->seqlen_q < 0 || p->seqlen_k < 0)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: negative batch/seqlen (%d, %d, %d)", p->batch, p->seqlen_q,
+                       p->seqlen_k);
+    if (p->heads_q <= 0 || p->heads_kv <= 0 || p->heads_q % p->heads_kv != 0)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: num_heads_kv (%d) must divide num_heads_q (%d)", p->heads_kv,
+                       p->heads_q);
+    if (!(p->softcap >= 0.f)) return set_err(MFA_ERR_INVALID, "mfa_fwd: softcap must be >= 0");
+    if (p->window_left < -1 || p->window_right < -1)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: window bounds must be >= -1");
+    if ((p->cu_seqlens_q == nullptr) != (p->cu_seqlens_k == nullptr))
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
+
+    plan->empty = (p->batch == 0 || p->seqlen_q == 0);
+    const int es = din == MFA_DTYPE_F32 ? 4 : 2;
+    const int oes = dout == MFA_DTYPE_F32 ? 4 : 2;
+    if (!plan->empty) {
+        if (!p->q || !p->k || !p->v || !p->o) return set_err(MFA_ERR_INVALID, "mfa_fwd: NULL tensor pointer");
+        if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
+            return set_err(MFA_ERR_INVALID, "mfa_fwd: q/k/v/o must be 16-byte aligned");
+        const int64_t in_al = 16 / es;  // elements per 16 bytes
+        const int64_t s_in[9] = {p->q_batch_stride, p->q_seq_stride, p->q_head_stride,
+                                 p->k_batch_stride, p->k_seq_stride, p->k_head_stride,
+                                 p->v_batch_stride, p->v_seq_stride, p->v_head_stride};
+        for (int i = 0; i < 9; ++i)
+            if (s_in[i] % in_al != 0)
+                return set_err(MFA_ERR_INVALID, "mfa_fwd: q/k/v strides must be multiples of %lld elements",
+                               (long long)in_al);
+        const int64_t out_al = oes == 4 ? 4 : 4;  // 4-element (8 or 16 byte) stores
+        if (p->o_batch_stride % out_al || p->o_seq_stride % out_al || p->o_head_stride % out_al)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd: o strides must be multiples of 4 elements");
+        if (p->alibi_slopes && !(p->alibi_batch_stride == 0 || p->alibi_batch_stride == p->heads_q))
+            return set_err(MFA_ERR_INVALID, "mfa_fwd: alibi_batch_stride must be 0 or heads_q");
+    }
+
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128;
+    const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);
+    if (din == MFA_DTYPE_F32)
+        plan->cfg = bias ? select32<true>(dp) : select32<false>(dp);
+    else if (din == MFA_DTYPE_BF16)
+        plan->cfg = bias ? select16<true, true>(dp) : select16<true, false>(dp);
+    else
+        plan->cfg = bias ? select16<false, true>(dp) : select16<false, false>(dp);
+
+    KArgs& a = plan->args;
+    memset(&a, 0, sizeof(a));
+    a.q = static_cast<const char*>(p->q);
+    a.k = static_cast<const char*>(p->k);
+    a.v = static_cast<const char*>(p->v);
+    a.o = static_cast<char*>(p->o);
+    a.qb = p->q_batch_stride; a.qs = p->q_seq_stride; a.qh = p->q_head_stride;
+    a.kb = p->k_batch_stride; a.ks = p->k_seq_stride; a.kh = p->k_head_stride;
+    a.vb = p->v_batch_stride; a.vs = p->v_seq_stride; a.vh = p->v_head_stride;
+    a.ob = p->o_batch_stride; a.os = p->o_seq_stride; a.oh = p->o_head_stride;
+    a.cu_q = p->cu_seqlens_q;
+    a.cu_k = p->cu_seqlens_k;
+    a.alibi = p->alibi_slopes;
+    a.alibi_bstride = p->alibi_batch_stride;
+    a.B = p->batch; a.Hq = p->heads_q; a.Hkv = p->heads_kv;
+    a.Lq = p->seqlen_q; a.Lk = p->seqlen_k; a.D = D;
+    a.scale = p->scale;
+    a.scale_log2 = p->scale * kLog2e;
+    a.softcap = p->softcap;
+    a.softcap_k = p->softcap > 0.f ? 2.f * kLog2e / p->softcap : 0.f;
+    // clamp windows so center +/- window cannot overflow int32
+    const int64_t wmax = (int64_t)p->seqlen_q + (int64_t)p->seqlen_k + 1;
+    a.wl = p->window_left < 0 ? -1 : (int32_t)(p->window_left > wmax ? wmax : p->window_left);
+    a.wr = p->window_right < 0 ? -1 : (int32_t)(p->window_right > wmax ? wmax : p->window_right);
+    a.causal = p->causal ? 1 : 0;
+    a.out_f32 = dout == MFA_DTYPE_F32 ? 1 : 0;
+
+    const int rows = plan->cfg.rows;
+    a.T = (p->seqlen_q + rows - 1) / rows;
+    a.U = p->batch * p->heads_q;
+    const int64_t G = (int64_t)p->batch * p->heads_kv;
+    if (G % 8 == 0 && G > 0) {
+        a.grouped = 1;
+        a.upx = (int32_t)(G / 8) * (p->heads_q / p->heads_kv);
+        plan->grid = 8 * a.upx * a.T;
+    } else {
+        a.grouped = 0;
+        a.upx = 0;
+        plan->grid = a.U * a.T;
+    }
+    if ((int64_t)a.U * a.T > 0x7fffffffLL / 2) return set_err(MFA_ERR_INVALID, "mfa_fwd: problem too large");
+    if (plan->grid == 0) plan->empty = true;
+    return MFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfa_abi_version(void) { return MFA_ABI_VERSION; }
+
+int mfa_params_size(void) { return (int)sizeof(mfa_fwd_params); }
+
+const char* mfa_last_error(void) { return g_err; }
+
+int mfa_supported(int32_t dtype_in, int32_t head_dim) {
+    if (dtype_in != MFA_DTYPE_F16 && dtype_in != MFA_DTYPE_BF16 && dtype_in != MFA_DTYPE_F32) return 0;
+    return head_dim > 0 && head_dim <= MFA_MAX_HEAD_DIM && head_dim % 8 == 0;
+}
+
+int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info) {
+    g_err[0] = 0;
+    if (!info) return set_err(MFA_ERR_INVALID, "mfa_fwd_launch_info: info is NULL");
+    Plan plan;
+    const int rc = make_plan(params, &plan);
+    if (rc != MFA_OK) return rc;
+    info->grid_x = plan.empty ? 0 : plan.grid;
+    info->block_x = kThreads;
+    info->rows_per_block = plan.cfg.rows;
+    info->keys_per_block = plan.cfg.keys;
+    info->lds_bytes = plan.cfg.lds;
+    snprintf(info->kernel_name, sizeof(info->kernel_name), "%s%s", plan.cfg.name,
+             (params->softcap > 0.f || params->alibi_slopes) ? "+bias" : "");
+    return MFA_OK;
+}
+
+int mfa_fwd(const mfa_fwd_params* params, void* stream) {
+    g_err[0] = 0;
+    Plan plan;
+    const int rc = make_plan(params, &plan);
+    if (rc != MFA_OK) return rc;
+    if (plan.empty) return MFA_OK;
+    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), plan.args);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd: launch failed: %s", hipGetErrorString(e));
+    return MFA_OK;
+}
+
+}  // extern "C"

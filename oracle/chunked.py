@@ -1,0 +1,139 @@
+"""ORACLE -- test infrastructure only, never product code.
+
+CPU restatement of the reference's chunked-fp32 torch path, the path every
+result of mtlflashattn_amd is checked against.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+module, and only as the checker or the CPU baseline.
+
+Follows, step for step:
+  * metal_flash_attn/_kernel.py:1165-1208 (`_flash_torch`): fp32 upcast
+    (:1172-1174); GQA by repeat_interleave of K/V (:1175-1178); query chunks of
+    MTLFLASHATTN_TORCH_CHUNK rows, default 2048 (:1156-1162, :1188); per chunk
+    scores = (q @ k^T) * scale (:1190) -> softcap (:1191-1192) -> ALiBi
+    (:1193-1196) -> causal / window masks (:1197-1204) -> softmax (:1205) ->
+    nan_to_num (:1206) -> @ V (:1207); cast to q.dtype (:1208, done by callers
+    through `cast_like`).
+  * metal_flash_attn/_kernel.py:1275-1285 (`_broadcast_alibi_slopes`).
+  * metal_flash_attn/__init__.py:62-99 (heads-third API, default scale
+    1/sqrt(D)) and :102-183 (varlen: one B=1 call per sequence, empty query
+    sequences skipped, [B, Hq] ALiBi rows picked per sequence).
+
+Pinned by tests/test_oracle_pinning.py against torch's SDPA (a library
+routine), an independent float64 C restatement of the streaming kernel
+(oracle/stream_ref.c), closed forms, and the committed fixtures in
+tests/golden/.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+DEFAULT_CHUNK = 2048
+
+
+def broadcast_alibi(alibi_slopes, B, Hq):
+    """[Hq] or [B, Hq] slopes -> contiguous [B*Hq] fp32 (_kernel.py:1275-1285)."""
+    s = alibi_slopes.detach().to(device="cpu", dtype=torch.float32)
+    if s.dim() == 1 and s.shape[0] == Hq:
+        s = s.unsqueeze(0).expand(B, Hq)
+    elif not (s.dim() == 2 and tuple(s.shape) == (B, Hq)):
+        raise ValueError(f"alibi_slopes must be [Hq={Hq}] or [B={B}, Hq={Hq}], got {tuple(s.shape)}")
+    return s.reshape(-1).contiguous()
+
+
+def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1, alibi=None,
+                chunk=DEFAULT_CHUNK, rows=None):
+    """Heads-second q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D] (CPU) -> fp32 [B,Hq,Lq,D].
+
+    `alibi` is the broadcast [B*Hq] fp32 slope vector or None.  The result is
+    the reference's fp32 `out` before its final cast.  `rows` optionally
+    restricts the computation to the query chunks whose start index is in
+    `rows` (other rows are left as NaN); each chunk is computed exactly as in
+    the full run, so the subset equals the corresponding rows of the full
+    result.
+    """
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
+    qf = q.detach().cpu().float()
+    kf = k.detach().cpu().float()
+    vf = v.detach().cpu().float()
+    if Hkv != Hq:
+        rep = Hq // Hkv
+        kf = kf.repeat_interleave(rep, dim=1)
+        vf = vf.repeat_interleave(rep, dim=1)
+    kt = kf.transpose(-1, -2)
+    out = torch.full((B, Hq, Lq, D), float("nan"), dtype=torch.float32)
+    chunk = max(1, int(chunk))
+    wl, wr = int(window_left), int(window_right)
+    windowed = wl >= 0 or wr >= 0
+    key_pos = torch.arange(Lk)[None, :] if (causal or windowed) else None
+    for start in range(0, Lq, chunk):
+        if rows is not None and start not in rows:
+            continue
+        end = min(start + chunk, Lq)
+        scores = (qf[:, :, start:end] @ kt) * scale
+        if softcap:
+            scores = softcap * torch.tanh(scores / softcap)
+        if alibi is not None:
+            center_a = torch.arange(start, end)[:, None] + (Lk - Lq)
+            key_a = torch.arange(Lk)[None, :]
+            scores = scores - alibi.reshape(B, Hq, 1, 1) * (center_a - key_a).abs().float()
+        if causal or windowed:
+            center = torch.arange(start, end)[:, None] + (Lk - Lq)
+            if causal:
+                scores = scores.masked_fill(key_pos > center, float("-inf"))
+            if wl >= 0:
+                scores = scores.masked_fill(key_pos < center - wl, float("-inf"))
+            if wr >= 0:
+                scores = scores.masked_fill(key_pos > center + wr, float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        probs = torch.nan_to_num(probs, nan=0.0)
+        out[:, :, start:end] = probs @ vf
+    return out
+
+
+def cast_like(out_f32, dtype):
+    """The reference's final `.to(q.dtype)` (_kernel.py:1208)."""
+    return out_f32.to(dtype)
+
+
+def flash_attn_func(q, k, v, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                    alibi_slopes=None, chunk=DEFAULT_CHUNK, rows=None):
+    """Heads-third q [B,Lq,Hq,D], k/v [B,Lk,Hkv,D] -> fp32 [B,Lq,Hq,D] (__init__.py:62-99)."""
+    B, _, Hq, D = q.shape
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    alibi = broadcast_alibi(alibi_slopes, B, Hq) if alibi_slopes is not None else None
+    out = flash_torch(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale, causal, softcap,
+                      window_size[0], window_size[1], alibi, chunk=chunk, rows=rows)
+    return out.transpose(1, 2).contiguous()
+
+
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, causal=False,
+                           window_size=(-1, -1), softcap=0.0, alibi_slopes=None, chunk=DEFAULT_CHUNK):
+    """Packed q [Tq,Hq,D], k/v [Tk,Hkv,D] -> fp32 [Tq,Hq,D] (__init__.py:102-183).
+
+    Rows of empty query sequences do not exist; rows of sequences with no
+    keys are 0.
+    """
+    cu_q = [int(x) for x in torch.as_tensor(cu_seqlens_q).tolist()]
+    cu_k = [int(x) for x in torch.as_tensor(cu_seqlens_k).tolist()]
+    Hq, D = q.shape[1], q.shape[2]
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    out = torch.zeros(q.shape, dtype=torch.float32)
+    for i in range(len(cu_q) - 1):
+        qs = q[cu_q[i]:cu_q[i + 1]]
+        ks = k[cu_k[i]:cu_k[i + 1]]
+        vs = v[cu_k[i]:cu_k[i + 1]]
+        if qs.shape[0] == 0:
+            continue
+        seq_alibi = alibi_slopes
+        if alibi_slopes is not None and alibi_slopes.dim() == 2:
+            seq_alibi = alibi_slopes[i]
+        alibi = broadcast_alibi(seq_alibi, 1, Hq) if seq_alibi is not None else None
+        o = flash_torch(qs.permute(1, 0, 2)[None], ks.permute(1, 0, 2)[None], vs.permute(1, 0, 2)[None],
+                        scale, causal, softcap, window_size[0], window_size[1], alibi, chunk=chunk)
+        out[cu_q[i]:cu_q[i + 1]] = o[0].permute(1, 0, 2)
+    return out
