@@ -14,6 +14,7 @@ import math
 
 import torch
 
+from . import _kernel
 from ._kernel import MAX_HEAD_DIM, flash_attn_forward, forward_bshd, forward_varlen
 from ._version import __version__
 
@@ -52,7 +53,7 @@ def _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, det
         raise NotImplementedError("mtlflashattn_amd: deterministic not supported")
     if return_attn_probs:
         raise NotImplementedError("mtlflashattn_amd: return_attn_probs not supported (probs never materialized)")
-    if q.device.type != "cuda" or torch.version.hip is None:
+    if not _kernel._is_rocm_tensor(q):
         raise NotImplementedError(f"mtlflashattn_amd: device {q.device.type!r} not supported (ROCm GPU only)")
     if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise NotImplementedError(f"mtlflashattn_amd: dtype {q.dtype} (q/k/v must match, fp16/bf16/fp32)")

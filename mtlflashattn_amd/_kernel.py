@@ -123,9 +123,14 @@ def _alibi_arg(alibi_slopes, B, Hq, device):
     return s.to(device=device, dtype=torch.float32).contiguous(), bstride
 
 
+def _is_rocm_tensor(t) -> bool:
+    """True for a tensor on a ROCm GPU (the only device the HIP path serves)."""
+    return t.device.type == "cuda" and torch.version.hip is not None
+
+
 def _check_device(*tensors):
     for t in tensors:
-        if t.device.type != "cuda" or torch.version.hip is None:
+        if not _is_rocm_tensor(t):
             raise NotImplementedError(
                 f"mtlflashattn_amd: device {t.device.type!r} not supported (ROCm GPU only)"
             )

@@ -1,0 +1,135 @@
+"""The C ABI of libmtlfa_hip.so (include/mfa.h) on CPU: the library loads,
+exports every function the header declares, agrees with the ctypes mirror of
+its parameter struct, and rejects invalid requests with an error code and a
+message before anything is launched.  No call here reaches a GPU: every
+mfa_fwd call fails validation or has an empty problem."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from mtlflashattn_amd import _build, _hip, _kernel
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "mfa.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_build.LIB_PATH):
+        _build.build()
+    return _hip.load()
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(mfa_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert set(declared_functions()) >= {"mfa_abi_version", "mfa_last_error", "mfa_supported", "mfa_fwd",
+                                         "mfa_fwd_launch_info", "mfa_params_size"}
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(_build.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(raw, name), f"{name} declared in include/mfa.h but not exported"
+
+
+def test_abi_version_and_struct_size(lib):
+    assert lib.mfa_abi_version() == _hip.MFA_ABI_VERSION
+    assert lib.mfa_params_size() == ctypes.sizeof(_hip.MfaFwdParams)
+    src = open(HEADER).read()
+    assert f"#define MFA_ABI_VERSION {_hip.MFA_ABI_VERSION}" in src
+    for name in ("MFA_DTYPE_F16", "MFA_DTYPE_BF16", "MFA_DTYPE_F32", "MFA_ERR_INVALID", "MFA_ERR_UNSUPPORTED"):
+        val = int(re.search(rf"#define {name} (-?\d+)", src).group(1))
+        assert val == getattr(_hip, name)
+
+
+def test_supported_table(lib):
+    for dt in (_hip.MFA_DTYPE_F16, _hip.MFA_DTYPE_BF16, _hip.MFA_DTYPE_F32):
+        assert all(lib.mfa_supported(dt, d) for d in (8, 32, 64, 96, 128))
+        assert not lib.mfa_supported(dt, 130) and not lib.mfa_supported(dt, 33) and not lib.mfa_supported(dt, 0)
+    assert not lib.mfa_supported(7, 64)
+
+
+def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
+    p = _hip.MfaFwdParams()
+    p.q = p.k = p.v = p.o = 4096
+    p.q_batch_stride, p.q_seq_stride, p.q_head_stride = L * H * D, H * D, D
+    p.k_batch_stride, p.k_seq_stride, p.k_head_stride = L * Hkv * D, Hkv * D, D
+    p.v_batch_stride, p.v_seq_stride, p.v_head_stride = L * Hkv * D, Hkv * D, D
+    p.o_batch_stride, p.o_seq_stride, p.o_head_stride = L * H * D, H * D, D
+    p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k, p.head_dim = B, H, Hkv, L, L, D
+    p.scale, p.softcap = 0.125, 0.0
+    p.window_left = p.window_right = -1
+    p.dtype_in = p.dtype_out = dtype
+    return p
+
+
+@pytest.mark.parametrize("mutate,code,msg", [
+    (lambda p: setattr(p, "dtype_in", 9), _hip.MFA_ERR_INVALID, "dtype_in"),
+    (lambda p: setattr(p, "dtype_out", _hip.MFA_DTYPE_F16), _hip.MFA_ERR_INVALID, "dtype_out"),
+    (lambda p: setattr(p, "head_dim", 160), _hip.MFA_ERR_UNSUPPORTED, "head_dim"),
+    (lambda p: setattr(p, "head_dim", 36), _hip.MFA_ERR_UNSUPPORTED, "multiple of 8"),
+    (lambda p: setattr(p, "heads_kv", 3), _hip.MFA_ERR_INVALID, "must divide"),
+    (lambda p: setattr(p, "softcap", -1.0), _hip.MFA_ERR_INVALID, "softcap"),
+    (lambda p: setattr(p, "window_left", -2), _hip.MFA_ERR_INVALID, "window"),
+    (lambda p: setattr(p, "q", 4098), _hip.MFA_ERR_INVALID, "aligned"),
+    (lambda p: setattr(p, "k_seq_stride", 68), _hip.MFA_ERR_INVALID, "strides"),
+    (lambda p: setattr(p, "o", None), _hip.MFA_ERR_INVALID, "NULL"),
+    (lambda p: setattr(p, "cu_seqlens_q", 256), _hip.MFA_ERR_INVALID, "cu_seqlens"),
+    (lambda p: setattr(p, "seqlen_k", -1), _hip.MFA_ERR_INVALID, "negative"),
+])
+def test_invalid_requests_are_rejected_before_launch(lib, mutate, code, msg):
+    p = good_params()
+    mutate(p)
+    assert lib.mfa_fwd(ctypes.byref(p), None) == code
+    assert msg in lib.mfa_last_error().decode()
+    with pytest.raises(_hip.HipLibraryError, match=msg):
+        _hip.fwd(p, 0)
+
+
+def test_null_params(lib):
+    assert lib.mfa_fwd(None, None) == _hip.MFA_ERR_INVALID
+    assert b"NULL" in lib.mfa_last_error()
+
+
+def test_empty_problem_is_a_no_op(lib):
+    p = good_params(B=0)
+    assert lib.mfa_fwd(ctypes.byref(p), None) == _hip.MFA_OK
+    assert lib.mfa_last_error() == b""
+    p = good_params()
+    p.seqlen_q = 0
+    assert lib.mfa_fwd(ctypes.byref(p), None) == _hip.MFA_OK
+
+
+def test_launch_geometry_of_the_baseline_configs(lib):
+    bf = torch.empty(1, 8192, 16, 64, dtype=torch.bfloat16)
+    info = _kernel.launch_info(bf, bf, bf)
+    assert info.block_x == 256 and info.grid_x * info.rows_per_block >= 8192 * 16
+    assert info.kernel_name.startswith(b"mfa_fwd16<bf16,d64")
+    # XCD-grouped schedule: grid is a multiple of 8 and covers every (head, tile)
+    assert info.grid_x % 8 == 0
+    f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
+    info = _kernel.launch_info(f16, f16, f16, causal=True)
+    assert info.kernel_name.startswith(b"mfa_fwd16<f16,d128")
+    big = torch.empty(1, 32768, 16, 128, dtype=torch.bfloat16)
+    info = _kernel.launch_info(big, big, big, causal=True, softcap=30.0, alibi=True, window_left=2048, window_right=0)
+    assert info.kernel_name.endswith(b"+bias")
+    f32 = torch.empty(1, 512, 2, 64, dtype=torch.float32)
+    info = _kernel.launch_info(f32, f32, f32)
+    assert info.kernel_name.startswith(b"mfa_fwd32<f32,d64")
+    assert info.grid_x == 2 * (512 // info.rows_per_block)  # linear schedule: heads x tiles
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setenv("MTLFLASHATTN_HIP_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_hip, "_lib", None)
+    with pytest.raises(_hip.HipLibraryError, match="not found"):
+        _hip.load()

@@ -1,0 +1,298 @@
+"""Pins the oracle (oracle/chunked.py, the reference's chunked-fp32 torch path
+restated) before anything is checked against it.
+
+The reference holds no golden vectors (its tests compare against a naive fp32
+statement, tests/test_flash_attn_func.py:12-49).  The oracle is pinned here by
+  * torch's scaled_dot_product_attention (a library routine) wherever the
+    semantics coincide (no softcap/ALiBi/window; causal only with Lq == Lk;
+    GQA through enable_gqa);
+  * oracle/stream_ref.c, a float64 two-pass evaluation of the reference's
+    scalar-kernel math (metal_flash_attn/_kernel.py:32-87) -- a different
+    evaluation order in a different language;
+  * closed forms that a plausible mistake breaks: a dropped or misplaced
+    softcap, a flipped ALiBi sign or missing |.|, a wrong bottom-right offset
+    (Lk - Lq), an off-by-one window bound, a top-left causal mask, a missing
+    scale, a transposed operand.
+All on CPU; sizes keep the whole file to a few seconds.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import chunked, stream
+
+ATOL = 1e-5
+
+
+def rnd(*shape, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def qkv(B, Hq, Hkv, Lq, Lk, D, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, Lq, D, generator=g) * scale
+    k = torch.randn(B, Hkv, Lk, D, generator=g) * scale
+    v = torch.randn(B, Hkv, Lk, D, generator=g) * scale
+    return q, k, v
+
+
+def close(a, b, atol=ATOL):
+    err = (a.double() - b.double()).abs().max().item() if a.numel() else 0.0
+    assert err <= atol, f"max abs err {err:.3e} > {atol}"
+
+
+# --------------------------------------------------------------------------- library cross-checks
+
+
+@pytest.mark.parametrize("D", [16, 64, 128])
+def test_plain_matches_sdpa(D):
+    q, k, v = qkv(2, 3, 3, 70, 90, D, seed=1)
+    ref = F.scaled_dot_product_attention(q, k, v)
+    close(chunked.flash_torch(q, k, v, 1 / math.sqrt(D), False), ref)
+
+
+def test_custom_scale_matches_sdpa():
+    q, k, v = qkv(1, 2, 2, 64, 64, 32, seed=2)
+    for s in (0.25, 1.0, 0.01):
+        close(chunked.flash_torch(q, k, v, s, False), F.scaled_dot_product_attention(q, k, v, scale=s))
+
+
+def test_causal_equal_lengths_matches_sdpa():
+    q, k, v = qkv(1, 4, 4, 97, 97, 64, seed=3)
+    close(chunked.flash_torch(q, k, v, 0.125, True), F.scaled_dot_product_attention(q, k, v, is_causal=True))
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 1), (6, 3)])
+def test_gqa_matches_sdpa_enable_gqa(hq, hkv):
+    q, k, v = qkv(2, hq, hkv, 40, 56, 32, seed=4)
+    ref = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+    close(chunked.flash_torch(q, k, v, 1 / math.sqrt(32), False), ref)
+
+
+def test_config1_matches_sdpa():
+    # BASELINE config 1 inputs: [1,512,2,64] fp32 from seed 0, scale 1/8
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 512, 2, 64, generator=g) for _ in range(3))
+    out = chunked.flash_attn_func(q, k, v, softmax_scale=0.125)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale=0.125)
+    close(out, ref.transpose(1, 2))
+
+
+# --------------------------------------------------------------------------- independent float64 restatement
+
+
+CASES = [
+    dict(causal=False),
+    dict(causal=True),
+    dict(causal=True, window_left=7),
+    dict(causal=False, window_left=5, window_right=3),
+    dict(causal=False, window_left=-1, window_right=2),
+    dict(causal=False, softcap=2.5),
+    dict(causal=True, softcap=30.0),
+    dict(causal=False, alibi="head"),
+    dict(causal=True, alibi="batch"),
+    dict(causal=True, window_left=9, softcap=4.0, alibi="head"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(i) for i in range(len(CASES))])
+@pytest.mark.parametrize("shape", [(2, 4, 2, 33, 33, 16), (1, 2, 2, 20, 45, 8), (1, 4, 1, 45, 20, 24)],
+                         ids=["square-gqa", "lq<lk", "lq>lk-mqa"])
+def test_matches_float64_stream(case, shape):
+    B, Hq, Hkv, Lq, Lk, D = shape
+    q, k, v = qkv(B, Hq, Hkv, Lq, Lk, D, seed=5)
+    kw = dict(case)
+    al = kw.pop("alibi", None)
+    alibi = None
+    if al == "head":
+        alibi = chunked.broadcast_alibi(torch.linspace(0.05, 0.6, Hq), B, Hq)
+    elif al == "batch":
+        alibi = chunked.broadcast_alibi(torch.rand(B, Hq, generator=torch.Generator().manual_seed(1)), B, Hq)
+    a = chunked.flash_torch(q, k, v, 0.3, alibi=alibi, **kw)
+    b = stream.stream_fwd(q, k, v, 0.3, alibi=alibi, **kw)
+    close(a, b)
+
+
+# --------------------------------------------------------------------------- closed forms
+
+
+def test_single_key_returns_its_value():
+    q, k, v = qkv(1, 2, 2, 9, 1, 16, seed=6)
+    out = chunked.flash_torch(q, k, v, 0.7, False)
+    close(out, v.expand(1, 2, 9, 16))
+
+
+def test_constant_values_return_the_constant():
+    q, k, _ = qkv(1, 2, 2, 30, 40, 16, seed=7)
+    row = rnd(16, seed=8)
+    v = row.expand(1, 2, 40, 16).contiguous()
+    for kw in (dict(causal=False), dict(causal=True), dict(causal=False, window_left=3, window_right=0),
+               dict(causal=False, softcap=1.0)):
+        out = chunked.flash_torch(q, k, v, 0.5, **kw)
+        close(out, row.expand_as(out))
+
+
+def test_zero_query_is_mean_of_values():
+    _, k, v = qkv(1, 2, 2, 24, 24, 16, seed=9)
+    q = torch.zeros(1, 2, 24, 16)
+    close(chunked.flash_torch(q, k, v, 0.9, False), v.mean(dim=2, keepdim=True).expand(1, 2, 24, 16))
+    # causal, Lq == Lk: row i averages keys 0..i (prefix means)
+    prefix = v.cumsum(dim=2) / torch.arange(1, 25).view(1, 1, 24, 1)
+    close(chunked.flash_torch(q, k, v, 0.9, True), prefix)
+
+
+def test_bottom_right_causal_with_lq_lt_lk():
+    # Lq=5, Lk=12: center = i + 7, so row 0 averages keys 0..7 when q = 0
+    _, k, v = qkv(1, 1, 1, 5, 12, 8, seed=10)
+    q = torch.zeros(1, 1, 5, 8)
+    out = chunked.flash_torch(q, k, v, 1.0, True)
+    for i in range(5):
+        close(out[0, 0, i], v[0, 0, : i + 8].mean(0))
+
+
+def test_causal_lq_gt_lk_zero_rows():
+    q, k, v = qkv(1, 2, 2, 12, 5, 8, seed=11)
+    out = chunked.flash_torch(q, k, v, 0.4, True)
+    assert torch.count_nonzero(out[:, :, :7]) == 0  # rows i < Lq-Lk see no key
+    assert not torch.isnan(out).any()
+    close(out[:, :, 7], v[:, :, 0])  # row Lq-Lk sees key 0 only
+
+
+@pytest.mark.parametrize("Lq,Lk", [(10, 10), (6, 14), (14, 6)])
+def test_window_zero_zero_picks_the_diagonal_key(Lq, Lk):
+    q, k, v = qkv(1, 2, 2, Lq, Lk, 8, seed=12)
+    out = chunked.flash_torch(q, k, v, 0.5, False, window_left=0, window_right=0)
+    for i in range(Lq):
+        c = i + Lk - Lq
+        if 0 <= c < Lk:
+            close(out[:, :, i], v[:, :, c])
+        else:
+            assert torch.count_nonzero(out[:, :, i]) == 0
+
+
+def test_window_one_zero_averages_two_keys():
+    _, k, v = qkv(1, 1, 1, 9, 9, 8, seed=13)
+    q = torch.zeros(1, 1, 9, 8)
+    out = chunked.flash_torch(q, k, v, 1.0, False, window_left=1, window_right=0)
+    close(out[0, 0, 0], v[0, 0, 0])
+    for i in range(1, 9):
+        close(out[0, 0, i], (v[0, 0, i - 1] + v[0, 0, i]) / 2)
+
+
+def test_window_minus_one_zero_is_causal_and_wide_window_is_full():
+    q, k, v = qkv(1, 2, 2, 20, 31, 16, seed=14)
+    assert torch.equal(chunked.flash_torch(q, k, v, 0.3, False, window_left=-1, window_right=0),
+                       chunked.flash_torch(q, k, v, 0.3, True))
+    assert torch.equal(chunked.flash_torch(q, k, v, 0.3, False, window_left=1000, window_right=1000),
+                       chunked.flash_torch(q, k, v, 0.3, False))
+
+
+@pytest.mark.parametrize("Lq,Lk", [(12, 12), (7, 15), (15, 7)])
+def test_alibi_huge_slope_selects_the_center_key(Lq, Lk):
+    q, k, v = qkv(1, 2, 2, Lq, Lk, 8, seed=15)
+    alibi = torch.full((2,), 1e3)
+    out = chunked.flash_torch(q, k, v, 0.1, False, alibi=alibi)
+    for i in range(Lq):
+        c = i + Lk - Lq
+        if 0 <= c < Lk:
+            close(out[:, :, i], v[:, :, c], atol=1e-4)
+
+
+def test_alibi_three_key_closed_form():
+    # q = 0: weights of query 1 are exp(-s*|1-j|) -> (e^-s v0 + v1 + e^-s v2) / (1 + 2 e^-s)
+    _, k, v = qkv(1, 1, 1, 3, 3, 4, seed=16)
+    q = torch.zeros(1, 1, 3, 4)
+    s = 0.7
+    out = chunked.flash_torch(q, k, v, 1.0, False, alibi=torch.tensor([s]))
+    e = math.exp(-s)
+    close(out[0, 0, 1], (e * v[0, 0, 0] + v[0, 0, 1] + e * v[0, 0, 2]) / (1 + 2 * e))
+    # query 0: exp(-s*j)
+    w = torch.tensor([1.0, e, e * e])
+    close(out[0, 0, 0], (w[:, None] * v[0, 0]).sum(0) / w.sum())
+
+
+def test_alibi_zero_slopes_is_plain():
+    q, k, v = qkv(2, 2, 2, 16, 16, 8, seed=17)
+    close(chunked.flash_torch(q, k, v, 0.4, True, alibi=torch.zeros(4)), chunked.flash_torch(q, k, v, 0.4, True))
+
+
+def test_softcap_limits():
+    q, k, v = qkv(1, 2, 2, 16, 24, 16, seed=18, scale=2.0)
+    # a huge cap is the identity on scores
+    close(chunked.flash_torch(q, k, v, 0.5, False, softcap=1e7), chunked.flash_torch(q, k, v, 0.5, False),
+          atol=1e-5)
+    # a tiny cap squashes every score into [-c, c]: uniform weights
+    close(chunked.flash_torch(q, k, v, 0.5, False, softcap=1e-7), v.mean(dim=2, keepdim=True).expand(1, 2, 16, 16))
+
+
+def test_softcap_two_key_closed_form():
+    q, k, v = qkv(1, 1, 1, 1, 2, 8, seed=19, scale=3.0)
+    c, scale = 2.0, 0.6
+    a = scale * float(q[0, 0, 0] @ k[0, 0, 0])
+    b = scale * float(q[0, 0, 0] @ k[0, 0, 1])
+    wa, wb = math.exp(c * math.tanh(a / c)), math.exp(c * math.tanh(b / c))
+    expect = (wa * v[0, 0, 0] + wb * v[0, 0, 1]) / (wa + wb)
+    close(chunked.flash_torch(q, k, v, scale, False, softcap=c)[0, 0, 0], expect)
+
+
+def test_softcap_applies_before_alibi():
+    # q = 0 makes every raw score 0; softcap(0) = 0, so only ALiBi remains:
+    # if the cap were applied after ALiBi the bias itself would be squashed.
+    _, k, v = qkv(1, 1, 1, 3, 3, 4, seed=20)
+    q = torch.zeros(1, 1, 3, 4)
+    with_cap = chunked.flash_torch(q, k, v, 1.0, False, softcap=0.01, alibi=torch.tensor([2.0]))
+    no_cap = chunked.flash_torch(q, k, v, 1.0, False, alibi=torch.tensor([2.0]))
+    close(with_cap, no_cap)
+
+
+def test_chunking_is_invisible():
+    q, k, v = qkv(1, 2, 2, 100, 77, 16, seed=21)
+    a = chunked.flash_torch(q, k, v, 0.3, True, softcap=5.0, alibi=torch.tensor([0.1, 0.2]), chunk=13)
+    b = chunked.flash_torch(q, k, v, 0.3, True, softcap=5.0, alibi=torch.tensor([0.1, 0.2]))
+    close(a, b, atol=1e-6)
+
+
+def test_row_subset_equals_full_rows():
+    q, k, v = qkv(1, 2, 2, 100, 60, 16, seed=22)
+    full = chunked.flash_torch(q, k, v, 0.3, True, chunk=32)
+    part = chunked.flash_torch(q, k, v, 0.3, True, chunk=32, rows={64})
+    assert torch.equal(part[:, :, 64:96], full[:, :, 64:96])
+    assert torch.isnan(part[:, :, :64]).all()
+
+
+def test_empty_keys_give_zero_rows():
+    q = rnd(1, 2, 5, 8, seed=23)
+    k = torch.zeros(1, 2, 0, 8)
+    out = chunked.flash_torch(q, k, k, 0.3, False)
+    assert out.shape == (1, 2, 5, 8) and torch.count_nonzero(out) == 0
+
+
+def test_varlen_rows_equal_dense_per_sequence():
+    lens_q, lens_k = [5, 0, 9, 3], [7, 4, 9, 0]
+    g = torch.Generator().manual_seed(24)
+    q = torch.randn(sum(lens_q), 4, 8, generator=g)
+    k = torch.randn(sum(lens_k), 2, 8, generator=g)
+    v = torch.randn(sum(lens_k), 2, 8, generator=g)
+    cu_q = [0] + list(torch.tensor(lens_q).cumsum(0).tolist())
+    cu_k = [0] + list(torch.tensor(lens_k).cumsum(0).tolist())
+    out = chunked.flash_attn_varlen_func(q, k, v, torch.tensor(cu_q), torch.tensor(cu_k), causal=True)
+    for i in range(4):
+        qs, ks, vs = q[cu_q[i]:cu_q[i + 1]], k[cu_k[i]:cu_k[i + 1]], v[cu_k[i]:cu_k[i + 1]]
+        if qs.shape[0] == 0:
+            continue
+        dense = stream.stream_fwd(qs.permute(1, 0, 2)[None], ks.permute(1, 0, 2)[None], vs.permute(1, 0, 2)[None],
+                                  1 / math.sqrt(8), True)[0].permute(1, 0, 2)
+        close(out[cu_q[i]:cu_q[i + 1]], dense)
+
+
+def test_alibi_broadcast_shapes():
+    assert torch.equal(chunked.broadcast_alibi(torch.tensor([1.0, 2.0]), 3, 2), torch.tensor([1.0, 2.0] * 3))
+    bh = torch.arange(6.0).reshape(3, 2)
+    assert torch.equal(chunked.broadcast_alibi(bh, 3, 2), torch.arange(6.0))
+    with pytest.raises(ValueError):
+        chunked.broadcast_alibi(torch.ones(3), 3, 2)
