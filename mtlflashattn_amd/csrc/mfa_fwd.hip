@@ -17,8 +17,8 @@
 //    lane-local multiply.  P^T is fed to the MFMA straight from the S^T
 //    accumulator registers (converted to bf16/f16 in registers); it never
 //    touches LDS.  The k-slot order of that MFMA follows the accumulator
-//    row order, and V^T is written to LDS in the same (bit-permuted) key
-//    order so that each lane still reads 16 contiguous bytes.
+//    row order; V stays row-major in LDS and its transposed operand is read
+//    with ds_read_b64_tr_b16 (gfx950 LDS transpose loads).
 //  * Q is staged through LDS once (coalesced global reads) and then lives in
 //    registers as the MFMA B operand.  K and V stream through two LDS buffers:
 //    the global loads of block j+1 are issued before the MFMAs of block j and
@@ -57,8 +57,18 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
 
 constexpr int kWaves = 4;
+// wavefronts per SIMD the 16-bit kernels are register-budgeted for
+#ifndef MFA_WAVES_PER_EU
+#define MFA_WAVES_PER_EU 2
+#endif
+// software-pipelined unmasked blocks (QB >= 2)
+#ifndef MFA_PIPELINE
+#define MFA_PIPELINE 1
+#endif
 constexpr int kThreads = kWaves * 64;
 constexpr float kLog2e = 1.4426950408889634f;
+// dword 3 of a gfx9 buffer resource (raw buffer, 32-bit data format)
+constexpr int kBufferDword3 = 0x00020000;
 
 // Kernel argument block (copied by value into the kernarg segment).
 struct KArgs {
@@ -195,115 +205,160 @@ __device__ __forceinline__ int key_hi(const KArgs& a, int c, int Lk) {
 }
 
 // ----------------------------------------------------------------------------
-// Online softmax over one K/V block of S^T accumulators (shared by the 16-bit
-// and fp32 kernels, which use the same 32x32 accumulator layout).
+// Online softmax on S^T accumulators (shared by the 16-bit and fp32 kernels,
+// which use the same 32x32 accumulator layout).
 //
-// s[qb][kb][r]: raw score of query (32*qb + lane%32) and key
-//   j + 32*kb + 4*(lane/32) + acc_row(r).
-// On return s holds the (unnormalised) probabilities p.
-template <int QB, int NKB, int DB, bool BIAS>
-__device__ __forceinline__ void softmax_block(const KArgs& a, f32x16_t (&s)[QB][NKB], f32x16_t (&o)[DB][QB],
-                                              float (&m_run)[QB], float (&l_part)[QB], const int (&center)[QB],
-                                              const int (&lo)[QB], const int (&hi)[QB], const float (&slope)[QB],
-                                              int j, int half, bool masked) {
+// For one 32-query block, s[kb][r] is the raw score of query (lane%32) and
+// key j + 32*kb + 4*(lane/32) + acc_row(r).  The softmax of one K/V block is
+//   transform  : scale / soft-cap / ALiBi (BIAS) and masking (MASKED)
+//   row max    : over the lane's keys, merged across the two half-waves
+//   update     : new running max, rescale factor alpha for O and l
+//   probs      : p = exp2(s*c - mu), rounded to 16 bits for the PV MFMA,
+//                l += sum(p) (of the rounded values)
+
+// per-lane state of the query row a lane owns
+struct RowState {
+    int center;  // bottom-right diagonal: q + Lk - Lq
+    int lo, hi;  // valid key interval [lo, hi]
+    float slope; // ALiBi slope (0 without ALiBi)
+    float m;     // running max (raw-score units without BIAS, natural-log units with)
+    float l;     // running row sum (this half-wave's keys)
+};
+
+template <int NKB, bool BIAS, bool MASKED>
+__device__ __forceinline__ void qb_transform(const KArgs& a, f32x16_t (&s)[NKB], const RowState& rs, int j,
+                                             int half) {
     if constexpr (BIAS) {
         // natural-log units: x = scale*s, soft-cap, ALiBi (_kernel.py:75-77)
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) s[qb][kb][r] *= a.scale;
+            for (int r = 0; r < 16; ++r) s[kb][r] *= a.scale;
         if (a.softcap > 0.f) {
             // c * tanh(x / c) = c - 2c / (exp(2x/c) + 1)
             const float c2 = -2.f * a.softcap;
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float e = fast_exp2(s[qb][kb][r] * a.softcap_k);
-                        s[qb][kb][r] = fmaf(c2, __builtin_amdgcn_rcpf(e + 1.f), a.softcap);
-                    }
+                for (int r = 0; r < 16; ++r) {
+                    const float e = fast_exp2(s[kb][r] * a.softcap_k);
+                    s[kb][r] = fmaf(c2, __builtin_amdgcn_rcpf(e + 1.f), a.softcap);
+                }
         }
         if (a.alibi) {
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb) {
-                    const float cf = (float)(center[qb] - (j + 32 * kb + 4 * half));
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        s[qb][kb][r] = fmaf(-slope[qb], fabsf(cf - (float)acc_row(r)), s[qb][kb][r]);
-                }
-        }
-    }
-    if (masked) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
-                const int kbase = j + 32 * kb + 4 * half;
+                const float cf = (float)(rs.center - (j + 32 * kb + 4 * half));
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kbase + acc_row(r);
-                    const bool ok = (key >= lo[qb]) & (key <= hi[qb]);
-                    s[qb][kb][r] = ok ? s[qb][kb][r] : -INFINITY;
-                }
+                for (int r = 0; r < 16; ++r) s[kb][r] = fmaf(-rs.slope, fabsf(cf - (float)acc_row(r)), s[kb][r]);
             }
-    }
-    const float c = BIAS ? kLog2e : a.scale_log2;
-    float mx[QB];
-    bool need = false;
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        float m = s[qb][0][0];
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) m = fmaxf(m, s[qb][kb][r]);
-        mx[qb] = max_halves(m);
-        need |= mx[qb] > m_run[qb];
-    }
-    if (__any(need)) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            const float mn = fmaxf(m_run[qb], mx[qb]);
-            const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2((m_run[qb] - mn) * c);
-            m_run[qb] = mn;
-            l_part[qb] *= alpha;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[db][qb][r] *= alpha;
         }
     }
+    if constexpr (MASKED) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        const float mu = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb] * c;
-        float acc = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb) {
+            const int kbase = j + 32 * kb + 4 * half;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(fmaf(s[qb][kb][r], c, -mu));
-                s[qb][kb][r] = p;
-                acc += p;
+                const int key = kbase + acc_row(r);
+                s[kb][r] = ((key >= rs.lo) & (key <= rs.hi)) ? s[kb][r] : -INFINITY;
             }
-        l_part[qb] += acc;
+        }
     }
+}
+
+template <int NKB>
+__device__ __forceinline__ float qb_max(const f32x16_t (&s)[NKB]) {
+    float m = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, s[kb][r]);
+    return max_halves(m);
+}
+
+// New running max from the block max mx; returns alpha (1 when the max did
+// not move) and sets mu so that p = exp2(s*c - mu).  Rows with no valid key
+// so far keep m = -inf and get mu = 0, so masked scores give p = 0.
+__device__ __forceinline__ float qb_update(RowState& rs, float mx, float c, float& mu) {
+    const float mn = fmaxf(rs.m, mx);
+    const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
+    rs.m = mn;
+    rs.l *= alpha;
+    mu = (mn == -INFINITY) ? 0.f : mn * c;
+    return alpha;
+}
+
+template <int DB>
+__device__ __forceinline__ void scale_rows(f32x16_t (&o)[DB], float alpha) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+}
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_t;
+
+// Two probabilities rounded to 16 bits, packed, and added (as rounded) to acc:
+// the row sum l is the sum of exactly the weights the PV MFMA consumes.
+template <bool IS_BF16>
+__device__ __forceinline__ uint32_t pack_and_sum(float p0, float p1, float& acc) {
+    if constexpr (IS_BF16) {
+        const bf16x2_t pk = {(__bf16)p0, (__bf16)p1};
+        const bf16x2_t one = {(__bf16)1.f, (__bf16)1.f};
+        acc = __builtin_amdgcn_fdot2_f32_bf16(pk, one, acc, false);
+        return __builtin_bit_cast(uint32_t, pk);
+    } else {
+        const f16x2_t pk = {(_Float16)p0, (_Float16)p1};
+        const f16x2_t one = {(_Float16)1.f, (_Float16)1.f};
+        acc = __builtin_amdgcn_fdot2(pk, one, acc, false);
+        return __builtin_bit_cast(uint32_t, pk);
+    }
+}
+
+// P^T B operands straight from the accumulators: pw[kb][st] holds
+// accumulator registers 8*st..8*st+7 of key block kb.
+template <int NKB, bool IS_BF16>
+__device__ __forceinline__ void qb_probs16(const f32x16_t (&s)[NKB], u32x4_t (&pw)[NKB][2], float& l, float mu,
+                                           float c) {
+    float acc = l;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float p0 = fast_exp2(fmaf(s[kb][8 * st + 2 * w], c, -mu));
+                const float p1 = fast_exp2(fmaf(s[kb][8 * st + 2 * w + 1], c, -mu));
+                pw[kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, acc);
+            }
+    l = acc;
+}
+
+template <int NKB>
+__device__ __forceinline__ void qb_probs32(f32x16_t (&s)[NKB], float& l, float mu, float c) {
+    float acc = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = fast_exp2(fmaf(s[kb][r], c, -mu));
+            s[kb][r] = p;
+            acc += p;
+        }
+    l += acc;
 }
 
 // Normalise and store O^T accumulators: lane (half, q) holds
 // d = 32*db + 8*g + 4*half + {0..3} for g = 0..3.
 template <int QB, int DB, bool IS_BF16>
-__device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32x16_t (&o)[DB][QB],
-                                          const float (&l_part)[QB], int qrow0, int lane) {
+__device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32x16_t (&o)[QB][DB],
+                                          const RowState (&rs)[QB], int qrow0, int lane) {
     const int l32 = lane & 31, half = lane >> 5;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        const float l = sum_halves(l_part[qb]);
+        const float l = sum_halves(rs[qb].l);
         const float inv = l > 0.f ? 1.f / l : 0.f;  // fully masked rows -> 0 (_kernel.py:85)
         const int qrow = qrow0 + 32 * qb + l32;
         if (qrow >= sv.Lq) continue;
@@ -313,8 +368,8 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
             for (int g = 0; g < 4; ++g) {
                 const int d = 32 * db + 8 * g + 4 * half;
                 if (d >= a.D) continue;
-                const float v0 = o[db][qb][4 * g + 0] * inv, v1 = o[db][qb][4 * g + 1] * inv;
-                const float v2 = o[db][qb][4 * g + 2] * inv, v3 = o[db][qb][4 * g + 3] * inv;
+                const float v0 = o[qb][db][4 * g + 0] * inv, v1 = o[qb][db][4 * g + 1] * inv;
+                const float v2 = o[qb][db][4 * g + 2] * inv, v3 = o[qb][db][4 * g + 3] * inv;
                 if (a.out_f32) {
                     float* dst = reinterpret_cast<float*>(sv.o) + (int64_t)qrow * a.os + d;
                     *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
@@ -336,20 +391,25 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
 //   DP  : head dim padded to a multiple of 32 (32, 64, 96, 128)
 //   QB  : 32-query column blocks per wavefront (workgroup rows = 4*32*QB)
 //   NKB : 32-key row blocks per K/V block (keys per block = 32*NKB)
+// With QB >= 2, unmasked blocks run software-pipelined: the QK^T MFMAs of
+// query block qb+1 and the PV MFMAs of query block qb-1 are interleaved with
+// the softmax VALU work of query block qb, so the matrix cores and the
+// vector ALU run concurrently within one wavefront.
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
-__global__ void __launch_bounds__(kThreads) mfa_fwd16_kernel(KArgs a) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MFA_WAVES_PER_EU)))
+mfa_fwd16_kernel(KArgs a) {
     constexpr int BM = kWaves * QB * 32;
     constexpr int BN = NKB * 32;
     constexpr int DS = DP / 16;  // QK^T k-steps
     constexpr int DB = DP / 32;  // O^T row blocks
-    constexpr int KST = DP + 8;  // K / Q LDS row stride (elements): +16 B against bank conflicts
-    constexpr int VST = BN + 8;  // V^T LDS row stride (elements)
+    constexpr int KST = DP + 8;  // K / V / Q LDS row stride (elements): +16 B against bank conflicts
+    constexpr int VST = DP + 8;
     constexpr int K_ELEMS = BN * KST;
-    constexpr int V_ELEMS = DP * VST;
+    constexpr int V_ELEMS = BN * VST;
     constexpr int KV_ELEMS = 2 * (K_ELEMS + V_ELEMS);
     constexpr int Q_ELEMS = BM * KST;
     constexpr int SMEM = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
-    constexpr int CPR = DP / 8;                          // 16-byte chunks per row
+    constexpr int CPR = DP / 8;                                 // 16-byte chunks per row
     constexpr int KCH = (BN * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
     typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
 
@@ -385,24 +445,24 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd16_kernel(KArgs a) {
     __syncthreads();
 
     // ---- per-lane query state
-    int center[QB], lo[QB], hi[QB];
-    float slope[QB], m_run[QB], l_part[QB];
+    RowState rs[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        center[qb] = wq0 + 32 * qb + l32 + dq;
-        lo[qb] = key_lo(a, center[qb]);
-        hi[qb] = key_hi(a, center[qb], Lk);
-        slope[qb] = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
-        m_run[qb] = -INFINITY;
-        l_part[qb] = 0.f;
+        rs[qb].center = wq0 + 32 * qb + l32 + dq;
+        rs[qb].lo = key_lo(a, rs[qb].center);
+        rs[qb].hi = key_hi(a, rs[qb].center, Lk);
+        rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+        rs[qb].m = -INFINITY;
+        rs[qb].l = 0.f;
     }
-    f32x16_t o[DB][QB];
+    f32x16_t o[QB][DB];
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][qb][r] = 0.f;
+            for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.f;
+    const float c = BIAS ? kLog2e : a.scale_log2;
 
     // ---- key range of the workgroup and of this wavefront
     const int qlast = min(q0 + BM, Lq) - 1;
@@ -415,41 +475,213 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd16_kernel(KArgs a) {
     const int w_lo_first = key_lo(a, wq0 + dq), w_lo_last = key_lo(a, wlast + dq);
     const int w_hi_first = key_hi(a, wq0 + dq, Lk), w_hi_last = key_hi(a, wlast + dq, Lk);
 
-    // ---- K/V streaming: global -> registers (block j+1) -> LDS buffer
+    // ---- K/V streaming: global -> registers (block j+1) -> LDS buffer.
+    // Buffer loads through a per-block resource whose size ends at the last
+    // valid key row: rows past the sequence read as zero in hardware, and a
+    // chunk past the head dim gets an offset beyond the resource (zero too),
+    // so the loads carry no per-chunk conditions and no 64-bit address math.
     u32x4_t kreg[KCH], vreg[KCH];
+    uint32_t koff[KCH], voff[KCH];
+    int lds_off[KCH];
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        const int cc = tid + kThreads * i;
+        const int row = cc / CPR, col = (cc % CPR) * 8;
+        const bool in = (cc < BN * CPR) && (col < D);
+        koff[i] = in ? (uint32_t)(((int64_t)row * a.ks + col) * 2) : 0x80000000u;
+        voff[i] = in ? (uint32_t)(((int64_t)row * a.vs + col) * 2) : 0x80000000u;
+        lds_off[i] = (cc < BN * CPR) ? row * KST + col : -1;
+    }
     auto gload = [&](int j) {
+        const int rows = min(Lk - j, BN);  // >= 1
+        const int kbytes = (int)(((int64_t)(rows - 1) * a.ks + D) * 2);
+        const int vbytes = (int)(((int64_t)(rows - 1) * a.vs + D) * 2);
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(sv.k + (int64_t)j * a.ks * 2), (short)0, kbytes, kBufferDword3);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(sv.v + (int64_t)j * a.vs * 2), (short)0, vbytes, kBufferDword3);
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = tid + kThreads * i;
-            const int row = c / CPR, col = (c % CPR) * 8;
-            const bool ok = (c < BN * CPR) && (j + row < Lk) && (col < D);
-            u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-            if (ok) {
-                kv = *reinterpret_cast<const u32x4_t*>(sv.k + ((int64_t)(j + row) * a.ks + col) * 2);
-                vv = *reinterpret_cast<const u32x4_t*>(sv.v + ((int64_t)(j + row) * a.vs + col) * 2);
-            }
-            kreg[i] = kv;
-            vreg[i] = vv;
+            kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
+            vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0);
         }
     };
     auto swrite = [&](int buf) {
         uint16_t* kbuf = smem + buf * K_ELEMS;
-        uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;
+        uint16_t* vbuf = smem + 2 * K_ELEMS + buf * V_ELEMS;
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = tid + kThreads * i;
-            if (c < BN * CPR) {
-                const int row = c / CPR, col = (c % CPR) * 8;
-                *reinterpret_cast<u32x4_t*>(kbuf + row * KST + col) = kreg[i];
-                const int p = (row & ~31) + vt_pos(row & 31);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t w = vreg[i][e];
-                    vtb[(col + 2 * e) * VST + p] = (uint16_t)(w & 0xffffu);
-                    vtb[(col + 2 * e + 1) * VST + p] = (uint16_t)(w >> 16);
-                }
+            if (KCH * kThreads == BN * CPR || lds_off[i] >= 0) {
+                *reinterpret_cast<u32x4_t*>(kbuf + lds_off[i]) = kreg[i];
+                *reinterpret_cast<u32x4_t*>(vbuf + lds_off[i]) = vreg[i];
             }
         }
+    };
+    // PV A operand (V^T rows d = 32*db + lane%32, the 8 keys this half-wave's
+    // accumulator registers 8*st..8*st+7 hold) from row-major V with two
+    // ds_read_b64_tr_b16: in each 16-lane group, lane i addresses 4 elements
+    // of key row (i/4) and lane j receives element j of rows 0..3.
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
+    const int tr_row = 4 * half + ((lane & 15) >> 2);
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    auto load_vf = [&](const uint16_t* vbuf, int db, int kb, int st) -> op_t {
+        const uint16_t* p0 = vbuf + (32 * kb + 16 * st + tr_row) * VST + 32 * db + tr_col;
+        const uint16_t* p1 = p0 + 8 * VST;
+        if constexpr (IS_BF16) {
+            typedef __attribute__((address_space(3))) bf16x4_t* lp;
+            const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p0));
+            const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p1));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+            typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+            typedef __attribute__((address_space(3))) fp16x4_t* lp;
+            const f16x4_t lo = __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p0)));
+            const f16x4_t hi = __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p1)));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+    auto mfma16 = [](const op_t& x, const op_t& y, const f32x16_t& acc) {
+        if constexpr (IS_BF16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, acc, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, acc, 0, 0, 0);
+    };
+
+    // Sequential block: all QK^T, then per query block transform/max/update
+    // (rescale only when some row's max moved) and probs, then all PV.
+    auto block_simple = [&](auto masked_tag, const uint16_t* kbuf, const uint16_t* vtb, int j) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        f32x16_t sacc[QB][NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[qb][kb][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < DS; ++s) {
+                const op_t kf = *reinterpret_cast<const op_t*>(kbuf + (32 * kb + l32) * KST + 16 * s + 8 * half);
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma16(kf, qf[qb][s], sacc[qb][kb]);
+            }
+        }
+        u32x4_t pw[QB][NKB][2];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            qb_transform<NKB, BIAS, MASKED>(a, sacc[qb], rs[qb], j, half);
+            const float mx = qb_max<NKB>(sacc[qb]);
+            const bool need = mx > rs[qb].m;
+            float mu;
+            const float alpha = qb_update(rs[qb], mx, c, mu);
+            if (__any(need)) scale_rows<DB>(o[qb], alpha);
+            qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu, c);
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const op_t vf = load_vf(vtb, db, kb, st);
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        o[qb][db] = mfma16(vf, __builtin_bit_cast(op_t, pw[qb][kb][st]), o[qb][db]);
+                }
+    };
+
+    // Software-pipelined unmasked block (QB >= 2).  Program order:
+    //   QK(0) | QK(1) + softmax(0) | PV(0) + softmax(1) | ... | PV(QB-1)
+    // where "+" means the MFMAs are issued one or two at a time between the
+    // chunks of the softmax (partial row max, running-max update, O rescale,
+    // 8-probability groups), each chunk fenced by sched_barrier so the
+    // compiler keeps the interleave: every MFMA then runs on the matrix core
+    // while the following softmax chunk runs on the vector ALU.
+    auto block_pipelined = [&](const uint16_t* kbuf, const uint16_t* vtb, int j) {
+        constexpr int kQK = NKB * DS;      // MFMAs of one QK^T
+        constexpr int kPV = DB * NKB * 2;  // MFMAs of one PV
+        constexpr int NCH = NKB + 1 + DB + 2 * NKB;  // softmax chunks
+        op_t kf[NKB][DS];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int s = 0; s < DS; ++s)
+                kf[kb][s] = *reinterpret_cast<const op_t*>(kbuf + (32 * kb + l32) * KST + 16 * s + 8 * half);
+        f32x16_t sacc[QB][NKB];
+        u32x4_t pw[QB][NKB][2];
+        op_t vf[DB][NKB][2];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[qb][kb][r] = 0.f;
+        // MFMA number mi of the group issued beside softmax(qb):
+        // first the QK^T of query block qb+1, then the PV of query block qb-1
+        auto issue = [&](int qb, int mi) {
+            if (qb + 1 < QB) {
+                if (mi < kQK) {
+                    const int kb = mi / DS, s = mi % DS;
+                    sacc[qb + 1][kb] = mfma16(kf[kb][s], qf[qb + 1][s], sacc[qb + 1][kb]);
+                    return;
+                }
+                mi -= kQK;
+            }
+            if (qb > 0) {
+                const int db = mi / (2 * NKB), kb = (mi / 2) % NKB, st = mi % 2;
+                o[qb - 1][db] = mfma16(vf[db][kb][st], __builtin_bit_cast(op_t, pw[qb - 1][kb][st]), o[qb - 1][db]);
+            }
+        };
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int s = 0; s < DS; ++s) sacc[0][kb] = mfma16(kf[kb][s], qf[0][s], sacc[0][kb]);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) vf[db][kb][st] = load_vf(vtb, db, kb, st);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const int nm = (qb + 1 < QB ? kQK : 0) + (qb > 0 ? kPV : 0);
+            qb_transform<NKB, BIAS, false>(a, sacc[qb], rs[qb], j, half);
+            float mpart = -INFINITY, alpha = 1.f, mu = 0.f;
+            bool moved = false;
+#pragma unroll
+            for (int ci = 0; ci < NCH; ++ci) {
+#pragma unroll
+                for (int mi = ci * nm / NCH; mi < (ci + 1) * nm / NCH; ++mi) issue(qb, mi);
+                if (ci < NKB) {  // partial row max over key block ci
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mpart = fmaxf(mpart, sacc[qb][ci][r]);
+                } else if (ci == NKB) {  // merge halves, new running max
+                    const float mx = max_halves(mpart);
+                    moved = __any(mx > rs[qb].m);
+                    alpha = qb_update(rs[qb], mx, c, mu);
+                } else if (ci < NKB + 1 + DB) {  // rescale O rows (only if some row's max moved)
+                    const int db = ci - NKB - 1;
+                    if (moved) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+                    }
+                } else {  // 8 probabilities of (kb, st)
+                    const int g = ci - NKB - 1 - DB, kb = g / 2, st = g % 2;
+                    float acc = rs[qb].l;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        const float p0 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w], c, -mu));
+                        const float p1 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w + 1], c, -mu));
+                        pw[qb][kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, acc);
+                    }
+                    rs[qb].l = acc;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < kPV; ++mi) issue(QB, mi);
     };
 
     if (nblk > 0) {
@@ -467,64 +699,20 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd16_kernel(KArgs a) {
         if (!skip) {
             const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
             const uint16_t* kbuf = smem + buf * K_ELEMS;
-            const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;
-            // S^T = K Q^T
-            f32x16_t sacc[QB][NKB];
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) sacc[qb][kb][r] = 0.f;
-#pragma unroll
-                for (int s = 0; s < DS; ++s) {
-                    const op_t kf = *reinterpret_cast<const op_t*>(kbuf + (32 * kb + l32) * KST + 16 * s + 8 * half);
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) {
-                        if constexpr (IS_BF16)
-                            sacc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][s], sacc[qb][kb], 0, 0, 0);
-                        else
-                            sacc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qb][s], sacc[qb][kb], 0, 0, 0);
-                    }
-                }
+            const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;  // row-major V
+            if (masked) {
+                block_simple(std::true_type{}, kbuf, vtb, j);
+            } else {
+                if constexpr (QB >= 2 && MFA_PIPELINE)
+                    block_pipelined(kbuf, vtb, j);
+                else
+                    block_simple(std::false_type{}, kbuf, vtb, j);
             }
-            softmax_block<QB, NKB, DB, BIAS>(a, sacc, o, m_run, l_part, center, lo, hi, slope, j, half, masked);
-            // P^T as MFMA B operands, straight from the accumulators
-            op_t pf[QB][NKB][2];
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                    for (int st = 0; st < 2; ++st)
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            if constexpr (IS_BF16)
-                                pf[qb][kb][st][i] = (__bf16)sacc[qb][kb][8 * st + i];
-                            else
-                                pf[qb][kb][st][i] = (_Float16)sacc[qb][kb][8 * st + i];
-                        }
-            // O^T += V^T P^T
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                    for (int st = 0; st < 2; ++st) {
-                        const op_t vf = *reinterpret_cast<const op_t*>(vtb + (32 * db + l32) * VST + 32 * kb + 16 * st + 8 * half);
-#pragma unroll
-                        for (int qb = 0; qb < QB; ++qb) {
-                            if constexpr (IS_BF16)
-                                o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb][kb][st], o[db][qb], 0, 0, 0);
-                            else
-                                o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[qb][kb][st], o[db][qb], 0, 0, 0);
-                        }
-                    }
         }
         if (more) swrite(buf ^ 1);
     }
 
-    store_out<QB, DB, IS_BF16>(a, sv, o, l_part, wq0, lane);
+    store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -581,19 +769,19 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
     }
     __syncthreads();
 
-    int center[QB], lo[QB], hi[QB];
-    float slope[QB], m_run[QB], l_part[QB];
-    center[0] = wq0 + l32 + dq;
-    lo[0] = key_lo(a, center[0]);
-    hi[0] = key_hi(a, center[0], Lk);
-    slope[0] = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
-    m_run[0] = -INFINITY;
-    l_part[0] = 0.f;
-    f32x16_t o[DB][QB];
+    RowState rs[QB];
+    rs[0].center = wq0 + l32 + dq;
+    rs[0].lo = key_lo(a, rs[0].center);
+    rs[0].hi = key_hi(a, rs[0].center, Lk);
+    rs[0].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+    rs[0].m = -INFINITY;
+    rs[0].l = 0.f;
+    f32x16_t o[QB][DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][0][r] = 0.f;
+        for (int r = 0; r < 16; ++r) o[0][db][r] = 0.f;
+    const float c = BIAS ? kLog2e : a.scale_log2;
 
     const int qlast = min(q0 + BM, Lq) - 1;
     const int klo = key_lo(a, q0 + dq);
@@ -609,9 +797,9 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
     auto gload = [&](int j) {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = tid + kThreads * i;
-            const int row = c / CPR, col = (c % CPR) * 4;
-            const bool ok = (c < BN * CPR) && (j + row < Lk) && (col < D);
+            const int cc = tid + kThreads * i;
+            const int row = cc / CPR, col = (cc % CPR) * 4;
+            const bool ok = (cc < BN * CPR) && (j + row < Lk) && (col < D);
             u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
             if (ok) {
                 kv = *reinterpret_cast<const u32x4_t*>(sv.k + ((int64_t)(j + row) * a.ks + col) * 4);
@@ -626,13 +814,46 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
         float* vbuf = smem + 2 * K_ELEMS + buf * V_ELEMS;
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = tid + kThreads * i;
-            if (c < BN * CPR) {
-                const int row = c / CPR, col = (c % CPR) * 4;
+            const int cc = tid + kThreads * i;
+            if (cc < BN * CPR) {
+                const int row = cc / CPR, col = (cc % CPR) * 4;
                 *reinterpret_cast<u32x4_t*>(kbuf + row * KST + col) = kreg[i];
                 *reinterpret_cast<u32x4_t*>(vbuf + row * VST + col) = vreg[i];
             }
         }
+    };
+    auto block = [&](auto masked_tag, const float* kbuf, const float* vbuf, int j) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        f32x16_t sacc[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < DH; s += 4) {
+                const float4 kf = *reinterpret_cast<const float4*>(kbuf + (32 * kb + l32) * KST + half * DH + s);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[s], sacc[kb], 0, 0, 0);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[s + 1], sacc[kb], 0, 0, 0);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[s + 2], sacc[kb], 0, 0, 0);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[s + 3], sacc[kb], 0, 0, 0);
+            }
+        }
+        qb_transform<NKB, BIAS, MASKED>(a, sacc, rs[0], j, half);
+        const float mx = qb_max<NKB>(sacc);
+        const bool need = mx > rs[0].m;
+        float mu;
+        const float alpha = qb_update(rs[0], mx, c, mu);
+        if (__any(need)) scale_rows<DB>(o[0], alpha);
+        qb_probs32<NKB>(sacc, rs[0].l, mu, c);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float vf = vbuf[(32 * kb + 4 * half + acc_row(r)) * VST + 32 * db + l32];
+                    o[0][db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf, sacc[kb][r], o[0][db], 0, 0, 0);
+                }
     };
 
     if (nblk > 0) {
@@ -651,36 +872,16 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
             const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
             const float* kbuf = smem + buf * K_ELEMS;
             const float* vbuf = smem + 2 * K_ELEMS + buf * V_ELEMS;
-            f32x16_t sacc[QB][NKB];
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[0][kb][r] = 0.f;
-#pragma unroll
-                for (int s = 0; s < DH; s += 4) {
-                    const float4 kf = *reinterpret_cast<const float4*>(kbuf + (32 * kb + l32) * KST + half * DH + s);
-                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[s], sacc[0][kb], 0, 0, 0);
-                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[s + 1], sacc[0][kb], 0, 0, 0);
-                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[s + 2], sacc[0][kb], 0, 0, 0);
-                    sacc[0][kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[s + 3], sacc[0][kb], 0, 0, 0);
-                }
-            }
-            softmax_block<QB, NKB, DB, BIAS>(a, sacc, o, m_run, l_part, center, lo, hi, slope, j, half, masked);
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float vf = vbuf[(32 * kb + 4 * half + acc_row(r)) * VST + 32 * db + l32];
-                        o[db][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf, sacc[0][kb][r], o[db][0], 0, 0, 0);
-                    }
+            if (masked)
+                block(std::true_type{}, kbuf, vbuf, j);
+            else
+                block(std::false_type{}, kbuf, vbuf, j);
         }
         if (more) swrite(buf ^ 1);
     }
 
     // fp32 output (out_f32 is implied for fp32 input)
-    store_out<QB, DB, true>(a, sv, o, l_part, wq0, lane);
+    store_out<QB, DB, true>(a, sv, o, rs, wq0, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -720,13 +921,30 @@ KernelCfg cfg32(const char* name) {
 }
 
 // tile configuration per (dtype, padded head dim, bias)
+// Tile shape per padded head dim: QB 32-query blocks per wavefront, NKB
+// 32-key blocks per K/V block (overridable at build time for tuning sweeps).
+#ifndef MFA_D32_TILE
+#define MFA_D32_TILE 2, 2
+#endif
+#ifndef MFA_D64_TILE
+#define MFA_D64_TILE 2, 2
+#endif
+#ifndef MFA_D96_TILE
+#define MFA_D96_TILE 1, 2
+#endif
+#ifndef MFA_D128_TILE
+#define MFA_D128_TILE 1, 1
+#endif
+#define MFA_STR2(...) #__VA_ARGS__
+#define MFA_STR(...) MFA_STR2(__VA_ARGS__)
+
 template <bool IS_BF16, bool BIAS>
 KernelCfg select16(int dp) {
     switch (dp) {
-        case 32: return cfg16<32, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32,q64,k64>" : "mfa_fwd16<f16,d32,q64,k64>");
-        case 64: return cfg16<64, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64,q64,k64>" : "mfa_fwd16<f16,d64,q64,k64>");
-        case 96: return cfg16<96, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d96,q32,k64>" : "mfa_fwd16<f16,d96,q32,k64>");
-        default: return cfg16<128, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d128,q32,k64>" : "mfa_fwd16<f16,d128,q32,k64>");
+        case 32: return cfg16<32, MFA_D32_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32," MFA_STR(MFA_D32_TILE) ">" : "mfa_fwd16<f16,d32," MFA_STR(MFA_D32_TILE) ">");
+        case 64: return cfg16<64, MFA_D64_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64," MFA_STR(MFA_D64_TILE) ">" : "mfa_fwd16<f16,d64," MFA_STR(MFA_D64_TILE) ">");
+        case 96: return cfg16<96, MFA_D96_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d96," MFA_STR(MFA_D96_TILE) ">" : "mfa_fwd16<f16,d96," MFA_STR(MFA_D96_TILE) ">");
+        default: return cfg16<128, MFA_D128_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d128," MFA_STR(MFA_D128_TILE) ">" : "mfa_fwd16<f16,d128," MFA_STR(MFA_D128_TILE) ">");
     }
 }
 template <bool BIAS>
