@@ -28,10 +28,10 @@
 //    entirely outside the range of every query of the workgroup, masked
 //    element-wise only on the boundary blocks of each wavefront, and
 //    untouched elsewhere.
-//  * O and l are rescaled only in blocks where some row's running max grew
-//    (a wave-uniform branch); the running max itself is always exact, so the
-//    largest probability of a row is exactly 1.0 and loses nothing when P is
-//    rounded to 16 bits for the PV MFMA.
+//  * O and l are rescaled only in blocks where some row's max grew by more
+//    than a factor 2 (a wave-uniform branch); the reference max then becomes
+//    every row's exact max, so probabilities stay <= 2 and the row's largest
+//    weight is within one binade of 1.0 when P is rounded to 16 bits.
 //  * Workgroups are ordered heaviest-tile-first (causal: last query tile
 //    first) and, where the number of K/V head groups is a multiple of 8,
 //    all tiles of one K/V head are placed on one XCD so its K/V stays in that
@@ -60,6 +60,19 @@ constexpr int kWaves = 4;
 // wavefronts per SIMD the 16-bit kernels are register-budgeted for
 #ifndef MFA_WAVES_PER_EU
 #define MFA_WAVES_PER_EU 2
+#endif
+// exp2-domain growth of a row max below which the wave keeps its previous
+// reference max (0: move whenever any row's max grows)
+#ifndef MFA_RESCALE_TAU
+#define MFA_RESCALE_TAU 1
+#endif
+// padding (elements) of the row-major V tile in LDS
+#ifndef MFA_V_PAD
+#define MFA_V_PAD 32
+#endif
+// issue the next blocks' K/V staging between the last PV MFMAs
+#ifndef MFA_STAGE_IN_PV
+#define MFA_STAGE_IN_PV 1
 #endif
 // software-pipelined unmasked blocks (QB >= 2)
 #ifndef MFA_PIPELINE
@@ -277,16 +290,24 @@ __device__ __forceinline__ float qb_max(const f32x16_t (&s)[NKB]) {
     return max_halves(m);
 }
 
-// New running max from the block max mx; returns alpha (1 when the max did
-// not move) and sets mu so that p = exp2(s*c - mu).  Rows with no valid key
-// so far keep m = -inf and get mu = 0, so masked scores give p = 0.
-__device__ __forceinline__ float qb_update(RowState& rs, float mx, float c, float& mu) {
-    const float mn = fmaxf(rs.m, mx);
-    const float alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
-    rs.m = mn;
-    rs.l *= alpha;
-    mu = (mn == -INFINITY) ? 0.f : mn * c;
-    return alpha;
+// Running-max update from the block max mx.  The reference max of the wave
+// moves (to every row's exact max) only when some row's max grew by more than
+// MFA_RESCALE_TAU in the exp2 domain; otherwise probabilities are taken
+// against the previous reference, so p <= 2^TAU.  O and l always use the same
+// reference, so the final O/l is unaffected.  Returns true when the reference
+// moved (wave-uniform); alpha is then the factor for O and l.  Rows with no
+// valid key so far keep m = -inf and get mu = 0, so masked scores give p = 0.
+__device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float& mu, float& alpha) {
+    const bool moved = __any((mx - rs.m) * c > (float)MFA_RESCALE_TAU);
+    alpha = 1.f;
+    if (moved) {
+        const float mn = fmaxf(rs.m, mx);
+        alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
+        rs.m = mn;
+        rs.l *= alpha;
+    }
+    mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
+    return moved;
 }
 
 template <int DB>
@@ -402,8 +423,10 @@ mfa_fwd16_kernel(KArgs a) {
     constexpr int BN = NKB * 32;
     constexpr int DS = DP / 16;  // QK^T k-steps
     constexpr int DB = DP / 32;  // O^T row blocks
-    constexpr int KST = DP + 8;  // K / V / Q LDS row stride (elements): +16 B against bank conflicts
-    constexpr int VST = DP + 8;
+    constexpr int KST = DP + 8;  // K / Q LDS row stride (elements): +16 B against bank conflicts
+    // V row stride: 2*VST = 64 (mod 256) bytes, so the 4 rows x 64 bytes that a
+    // half-wave's transpose read touches fall on disjoint banks
+    constexpr int VST = DP + MFA_V_PAD;
     constexpr int K_ELEMS = BN * KST;
     constexpr int V_ELEMS = BN * VST;
     constexpr int KV_ELEMS = 2 * (K_ELEMS + V_ELEMS);
@@ -482,7 +505,7 @@ mfa_fwd16_kernel(KArgs a) {
     // so the loads carry no per-chunk conditions and no 64-bit address math.
     u32x4_t kreg[KCH], vreg[KCH];
     uint32_t koff[KCH], voff[KCH];
-    int lds_off[KCH];
+    int lds_off[KCH], vlds_off[KCH];
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
         const int cc = tid + kThreads * i;
@@ -491,6 +514,7 @@ mfa_fwd16_kernel(KArgs a) {
         koff[i] = in ? (uint32_t)(((int64_t)row * a.ks + col) * 2) : 0x80000000u;
         voff[i] = in ? (uint32_t)(((int64_t)row * a.vs + col) * 2) : 0x80000000u;
         lds_off[i] = (cc < BN * CPR) ? row * KST + col : -1;
+        vlds_off[i] = (cc < BN * CPR) ? row * VST + col : -1;
     }
     auto gload = [&](int j) {
         const int rows = min(Lk - j, BN);  // >= 1
@@ -513,7 +537,7 @@ mfa_fwd16_kernel(KArgs a) {
         for (int i = 0; i < KCH; ++i) {
             if (KCH * kThreads == BN * CPR || lds_off[i] >= 0) {
                 *reinterpret_cast<u32x4_t*>(kbuf + lds_off[i]) = kreg[i];
-                *reinterpret_cast<u32x4_t*>(vbuf + lds_off[i]) = vreg[i];
+                *reinterpret_cast<u32x4_t*>(vbuf + vlds_off[i]) = vreg[i];
             }
         }
     };
@@ -570,11 +594,8 @@ mfa_fwd16_kernel(KArgs a) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
             qb_transform<NKB, BIAS, MASKED>(a, sacc[qb], rs[qb], j, half);
-            const float mx = qb_max<NKB>(sacc[qb]);
-            const bool need = mx > rs[qb].m;
-            float mu;
-            const float alpha = qb_update(rs[qb], mx, c, mu);
-            if (__any(need)) scale_rows<DB>(o[qb], alpha);
+            float mu, alpha;
+            if (qb_update(rs[qb], qb_max<NKB>(sacc[qb]), c, mu, alpha)) scale_rows<DB>(o[qb], alpha);
             qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu, c);
         }
 #pragma unroll
@@ -597,7 +618,7 @@ mfa_fwd16_kernel(KArgs a) {
     // 8-probability groups), each chunk fenced by sched_barrier so the
     // compiler keeps the interleave: every MFMA then runs on the matrix core
     // while the following softmax chunk runs on the vector ALU.
-    auto block_pipelined = [&](const uint16_t* kbuf, const uint16_t* vtb, int j) {
+    auto block_pipelined = [&](const uint16_t* kbuf, const uint16_t* vtb, int j, auto&& tail) {
         constexpr int kQK = NKB * DS;      // MFMAs of one QK^T
         constexpr int kPV = DB * NKB * 2;  // MFMAs of one PV
         constexpr int NCH = NKB + 1 + DB + 2 * NKB;  // softmax chunks
@@ -657,9 +678,7 @@ mfa_fwd16_kernel(KArgs a) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) mpart = fmaxf(mpart, sacc[qb][ci][r]);
                 } else if (ci == NKB) {  // merge halves, new running max
-                    const float mx = max_halves(mpart);
-                    moved = __any(mx > rs[qb].m);
-                    alpha = qb_update(rs[qb], mx, c, mu);
+                    moved = qb_update(rs[qb], max_halves(mpart), c, mu, alpha);
                 } else if (ci < NKB + 1 + DB) {  // rescale O rows (only if some row's max moved)
                     const int db = ci - NKB - 1;
                     if (moved) {
@@ -680,36 +699,55 @@ mfa_fwd16_kernel(KArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        // last PV: the K/V staging of the next blocks (LDS stores, global
+        // loads) is issued between its MFMAs, which then run underneath it
 #pragma unroll
-        for (int mi = 0; mi < kPV; ++mi) issue(QB, mi);
+        for (int mi = 0; mi < kPV; ++mi) {
+            issue(QB, mi);
+            if (mi == 0) tail();
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
+    // Block it is computed from LDS buffer it%2 while the registers hold
+    // block it+1 (loaded during block it-1): its LDS stores and the global
+    // loads of block it+2 are issued during block it, one barrier per block.
     if (nblk > 0) {
         gload(jbeg);
         swrite(0);
+        if (nblk > 1) gload(jbeg + BN);
+        __syncthreads();
     }
     for (int it = 0; it < nblk; ++it) {
         const int j = jbeg + it * BN;
         const int buf = it & 1;
-        const bool more = it + 1 < nblk;
-        if (more) gload(j + BN);
-        __syncthreads();
-
+        auto stage_next = [&]() {
+            if (it + 1 < nblk) swrite(buf ^ 1);
+            if (it + 2 < nblk) gload(j + 2 * BN);
+        };
         const bool skip = !wave_live || (j + BN - 1 < w_lo_first) || (j > w_hi_last);
-        if (!skip) {
-            const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
-            const uint16_t* kbuf = smem + buf * K_ELEMS;
-            const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;  // row-major V
-            if (masked) {
-                block_simple(std::true_type{}, kbuf, vtb, j);
-            } else {
-                if constexpr (QB >= 2 && MFA_PIPELINE)
-                    block_pipelined(kbuf, vtb, j);
+        const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
+        const uint16_t* kbuf = smem + buf * K_ELEMS;
+        const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;  // row-major V
+        if (QB >= 2 && MFA_PIPELINE && !skip && !masked) {
+            if constexpr (QB >= 2 && MFA_PIPELINE) {
+                if constexpr (MFA_STAGE_IN_PV) {
+                    block_pipelined(kbuf, vtb, j, stage_next);
+                } else {
+                    block_pipelined(kbuf, vtb, j, [] {});
+                    stage_next();
+                }
+            }
+        } else {
+            if (!skip) {
+                if (masked)
+                    block_simple(std::true_type{}, kbuf, vtb, j);
                 else
                     block_simple(std::false_type{}, kbuf, vtb, j);
             }
+            stage_next();
         }
-        if (more) swrite(buf ^ 1);
+        __syncthreads();
     }
 
     store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
@@ -839,11 +877,8 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
             }
         }
         qb_transform<NKB, BIAS, MASKED>(a, sacc, rs[0], j, half);
-        const float mx = qb_max<NKB>(sacc);
-        const bool need = mx > rs[0].m;
-        float mu;
-        const float alpha = qb_update(rs[0], mx, c, mu);
-        if (__any(need)) scale_rows<DB>(o[0], alpha);
+        float mu, alpha;
+        if (qb_update(rs[0], qb_max<NKB>(sacc), c, mu, alpha)) scale_rows<DB>(o[0], alpha);
         qb_probs32<NKB>(sacc, rs[0].l, mu, c);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
@@ -910,7 +945,7 @@ struct KernelCfg {
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
 KernelCfg cfg16(const char* name) {
     constexpr int BM = kWaves * QB * 32, BN = NKB * 32;
-    constexpr int kv = 2 * (BN * (DP + 8) + DP * (BN + 8)), qs = BM * (DP + 8);
+    constexpr int kv = 2 * (BN * (DP + 8) + BN * (DP + MFA_V_PAD)), qs = BM * (DP + 8);
     return KernelCfg{mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs), name};
 }
 template <int DP, int NKB, bool BIAS>
@@ -933,7 +968,7 @@ KernelCfg cfg32(const char* name) {
 #define MFA_D96_TILE 1, 2
 #endif
 #ifndef MFA_D128_TILE
-#define MFA_D128_TILE 1, 1
+#define MFA_D128_TILE 1, 2
 #endif
 #define MFA_STR2(...) #__VA_ARGS__
 #define MFA_STR(...) MFA_STR2(__VA_ARGS__)
