@@ -31,10 +31,25 @@ if REPO not in sys.path:
 
 METRIC = "attn fwd effective TFLOP/s + % MFMA peak, bf16 H=16 D=64/128 L=8k, 1 MI355X"
 PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA
-# HBM bytes per launch measured by rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE, scaled
-# by the copy-kernel calibration factor) for the default workload; None until
-# measured.  See profiles/ for the runs these come from.
-TRAFFIC_BYTES = {}
+COPY_BYTES = 256 * 2**20  # calibration copy: bytes read = bytes written
+
+
+def measured_traffic(cfg: int):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of this config.
+
+    profiles/*_cfg<N>.md record FETCH_SIZE and WRITE_SIZE per dispatch, each
+    scaled by what the same counter reads for a plain 256 MiB device copy
+    (bench.py --copy-calibration), as `traffic_bytes_per_launch: <int>`.
+    Returns None when no summary exists.
+    """
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", f"*_cfg{cfg}.md"))):
+        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", open(path).read(), re.M)
+        if m:
+            return int(m.group(1))
+    return None
 
 
 def make_config(cfg: int):
@@ -158,6 +173,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after timing, run one plain 256 MiB device copy (rocprofv3 PMC calibration of "
+                         "FETCH_SIZE / WRITE_SIZE against known bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "bench.py measures one GPU only: this build's path is single-GPU "
@@ -206,7 +224,7 @@ def main():
                                    window_left=c["kw"].get("window_size", (-1, -1))[0],
                                    window_right=c["kw"].get("window_size", (-1, -1))[1])
         kname = info.kernel_name.decode()
-    traffic = TRAFFIC_BYTES.get(args.config)
+    traffic = measured_traffic(args.config)
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -227,6 +245,12 @@ def main():
                      "kernel_ms": round(kernel_ms, 4),
                      "note": "algorithmic FLOPs (4*D per valid (query,key) pair) / mean launch time"},
     }
+    if args.copy_calibration:
+        x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        y.copy_(x)
+        torch.cuda.synchronize()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.config)
     print(json.dumps(line), flush=True)

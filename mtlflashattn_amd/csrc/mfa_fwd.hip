@@ -32,10 +32,10 @@
 //    than a factor 2 (a wave-uniform branch); the reference max then becomes
 //    every row's exact max, so probabilities stay <= 2 and the row's largest
 //    weight is within one binade of 1.0 when P is rounded to 16 bits.
-//  * Workgroups are ordered heaviest-tile-first (causal: last query tile
-//    first) and, where the number of K/V head groups is a multiple of 8,
-//    all tiles of one K/V head are placed on one XCD so its K/V stays in that
-//    XCD's L2.
+//  * Where the number of K/V head groups is a multiple of 8, all tiles of one
+//    K/V head run on one XCD, one (sequence, q head) after another, so its K/V
+//    stays in that XCD's L2; within a head the heaviest tiles (causal: the
+//    last query tiles) go first.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -145,11 +145,13 @@ __device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int
     if (a.grouped) {
         // workgroup ids are dealt round-robin over the 8 XCDs; XCD x owns the
         // K/V head groups g = b*Hkv + hkv with g % 8 == x, all their q heads
-        // and all their tiles.
+        // and all their tiles.  Within an XCD the order is unit-major (all
+        // tiles of one (sequence, q head), heaviest first, then the next), so
+        // the workgroups resident on the XCD share one head's K/V in its L2.
         const int xcd = bid & 7;
         const int slot = bid >> 3;
-        tt = slot / a.upx;
-        const int j = slot - tt * a.upx;
+        const int j = slot / a.T;
+        tt = slot - j * a.T;
         const int R = a.Hq / a.Hkv;
         const int jg = j / R;
         const int g = xcd + 8 * jg;
