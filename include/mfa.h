@@ -50,6 +50,11 @@ extern "C" {
 
 #define MFA_MAX_HEAD_DIM 128
 
+/* tile_hint values (bf16/fp16 only; fp32 has one kernel) */
+#define MFA_TILE_AUTO 0     /* library's choice */
+#define MFA_TILE_256 1      /* 256-row tiles, 4 wavefronts */
+#define MFA_TILE_PINGPONG 2 /* 512-row ping-pong tiles, 8 wavefronts (head_dim <= 64) */
+
 /*
  * Forward parameters.  Replaces the SH/PR/AL buffers of the reference
  * (metal_flash_attn/_kernel.py:1221-1272) and the heads-second tensor
@@ -108,7 +113,8 @@ typedef struct mfa_fwd_params {
 
     int32_t dtype_in;  /* MFA_DTYPE_* of q, k and v */
     int32_t dtype_out; /* == dtype_in, or MFA_DTYPE_F32 (full-precision output) */
-    int32_t reserved;
+    int32_t tile_hint; /* MFA_TILE_AUTO (0); the others force a bf16/fp16 kernel
+                          (tests and tuning; results are the same either way) */
 } mfa_fwd_params;
 
 /* Launch geometry of one mfa_fwd call (for profiling/roofline reports). */

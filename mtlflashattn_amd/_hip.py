@@ -29,6 +29,9 @@ MFA_OK = 0
 MFA_ERR_INVALID = -1
 MFA_ERR_UNSUPPORTED = -2
 MFA_ERR_LAUNCH = -3
+MFA_TILE_AUTO = 0
+MFA_TILE_256 = 1
+MFA_TILE_PINGPONG = 2
 
 DTYPE_CODES = {
     torch.float16: MFA_DTYPE_F16,
@@ -56,7 +59,7 @@ class MfaFwdParams(ctypes.Structure):
         ("scale", ctypes.c_float), ("softcap", ctypes.c_float),
         ("window_left", _c_i32), ("window_right", _c_i32), ("causal", _c_i32),
         ("alibi_slopes", _c_ptr), ("alibi_batch_stride", _c_i32),
-        ("dtype_in", _c_i32), ("dtype_out", _c_i32), ("reserved", _c_i32),
+        ("dtype_in", _c_i32), ("dtype_out", _c_i32), ("tile_hint", _c_i32),
     ]
 
 

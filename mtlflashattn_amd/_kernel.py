@@ -43,6 +43,12 @@ _KNOWN_MODES = frozenset(
 _warned_modes = set()
 
 
+# Preferred C-ABI tile_hint for bf16/fp16 launches (0 = the library's choice);
+# tests set it to run every case through each kernel.  A preference the
+# launch cannot take (fp32, ping-pong with head_dim > 64) falls back to 0.
+_TILE_HINT = 0
+
+
 def _kernel_mode() -> str:
     mode = os.environ.get("MTLFLASHATTN_KERNEL", "auto").lower()
     if mode not in ("auto", "hip") and mode not in _warned_modes:
@@ -202,6 +208,10 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
         p.alibi_batch_stride = alibi_bstride
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
+    hint = _TILE_HINT
+    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and Dp > 64):
+        hint = _hip.MFA_TILE_AUTO
+    p.tile_hint = hint
     with torch.cuda.device(q.device):
         _hip.fwd(p, torch.cuda.current_stream(q.device).cuda_stream)
     if dst is not out:

@@ -74,6 +74,22 @@ constexpr int kWaves = 4;
 #ifndef MFA_STAGE_IN_PV
 #define MFA_STAGE_IN_PV 1
 #endif
+// stage the next blocks without branches in the pipelined path
+#ifndef MFA_BRANCHFREE_STAGE
+#define MFA_BRANCHFREE_STAGE 1
+#endif
+// raise the wave priority around the MFMA-only stretches of a pipelined block
+#ifndef MFA_SETPRIO
+#define MFA_SETPRIO 0
+#endif
+// fragments read ahead of their MFMAs in the ping-pong kernel's MFMA phase
+#ifndef MFA_PP_AHEAD
+#define MFA_PP_AHEAD 2
+#endif
+// raise the wave priority during the MFMA phase of the ping-pong kernel
+#ifndef MFA_PP_PRIO
+#define MFA_PP_PRIO 1
+#endif
 // software-pipelined unmasked blocks (QB >= 2)
 #ifndef MFA_PIPELINE
 #define MFA_PIPELINE 1
@@ -125,6 +141,30 @@ __device__ __forceinline__ float max_halves(float x) {
 __device__ __forceinline__ float sum_halves(float x) {
     auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
     return __int_as_float(sw[0]) + __int_as_float(sw[1]);
+}
+
+// Direct-to-LDS load (buffer_load_dwordx4 ... lds): lane i of the wave
+// writes the 16 bytes at `off` of the resource to dst + 16*i bytes (dst is
+// wave-uniform; an offset beyond the resource writes zeros).  Issued from
+// inline asm: the compiler does not see an LDS write, so it adds no vmcnt(0)
+// before later LDS reads it cannot prove disjoint.  The caller waits (vmcnt) before a
+// barrier that publishes the data.  The resource is a raw buffer: base
+// address, stride 0, `bytes` records, dword3 0x00020000.
+__device__ __forceinline__ void lds_load16(uint64_t base, uint32_t bytes, uint16_t* dst, uint32_t off) {
+    typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t rsrc_t;
+    const rsrc_t r = {(uint32_t)base, (uint32_t)(base >> 32) & 0xffffu, bytes, (uint32_t)kBufferDword3};
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(off), "s"(r)
+                 : "memory", "m0");
+}
+
+// Empty asm that reads and rewrites x in registers: pure arithmetic can be
+// moved across an asm barrier, but not across a pin of its inputs or outputs.
+template <class T>
+__device__ __forceinline__ void pin(T& x) {
+    asm volatile("" : "+v"(x));
 }
 
 // Accumulator row of register r in the 32x32 MFMA C layout, minus the
@@ -282,14 +322,19 @@ __device__ __forceinline__ void qb_transform(const KArgs& a, f32x16_t (&s)[NKB],
     }
 }
 
+// (two independent max chains, so consecutive instructions do not wait on
+// each other's results)
 template <int NKB>
 __device__ __forceinline__ float qb_max(const f32x16_t (&s)[NKB]) {
-    float m = s[0][0];
+    float m0 = s[0][0], m1 = s[0][1];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, s[kb][r]);
-    return max_halves(m);
+        for (int r = 0; r < 16; r += 2) {
+            m0 = fmaxf(m0, s[kb][r]);
+            m1 = fmaxf(m1, s[kb][r + 1]);
+        }
+    return max_halves(fmaxf(m0, m1));
 }
 
 // Running-max update from the block max mx.  The reference max of the wave
@@ -308,6 +353,19 @@ __device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float
         rs.m = mn;
         rs.l *= alpha;
     }
+    mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
+    return moved;
+}
+
+// qb_update without a branch: the same result, with the rescale of O left
+// to the caller (needed exactly when it returns true).
+__device__ __forceinline__ bool qb_update_flat(RowState& rs, float mx, float c, float& mu, float& alpha) {
+    const bool moved = __any((mx - rs.m) * c > (float)MFA_RESCALE_TAU);
+    const float mn = fmaxf(rs.m, mx);
+    const float a_ = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
+    alpha = moved ? a_ : 1.f;
+    rs.m = moved ? mn : rs.m;
+    rs.l *= alpha;
     mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
     return moved;
 }
@@ -345,7 +403,7 @@ __device__ __forceinline__ uint32_t pack_and_sum(float p0, float p1, float& acc)
 template <int NKB, bool IS_BF16>
 __device__ __forceinline__ void qb_probs16(const f32x16_t (&s)[NKB], u32x4_t (&pw)[NKB][2], float& l, float mu,
                                            float c) {
-    float acc = l;
+    float acc[2] = {l, 0.f};  // two independent sum chains
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -354,23 +412,23 @@ __device__ __forceinline__ void qb_probs16(const f32x16_t (&s)[NKB], u32x4_t (&p
             for (int w = 0; w < 4; ++w) {
                 const float p0 = fast_exp2(fmaf(s[kb][8 * st + 2 * w], c, -mu));
                 const float p1 = fast_exp2(fmaf(s[kb][8 * st + 2 * w + 1], c, -mu));
-                pw[kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, acc);
+                pw[kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, acc[w & 1]);
             }
-    l = acc;
+    l = acc[0] + acc[1];
 }
 
 template <int NKB>
 __device__ __forceinline__ void qb_probs32(f32x16_t (&s)[NKB], float& l, float mu, float c) {
-    float acc = 0.f;
+    float acc[2] = {0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const float p = fast_exp2(fmaf(s[kb][r], c, -mu));
             s[kb][r] = p;
-            acc += p;
+            acc[r & 1] += p;
         }
-    l += acc;
+    l += acc[0] + acc[1];
 }
 
 // Normalise and store O^T accumulators: lane (half, q) holds
@@ -519,9 +577,14 @@ mfa_fwd16_kernel(KArgs a) {
         vlds_off[i] = (cc < BN * CPR) ? row * VST + col : -1;
     }
     auto gload = [&](int j) {
-        const int rows = min(Lk - j, BN);  // >= 1
-        const int kbytes = (int)(((int64_t)(rows - 1) * a.ks + D) * 2);
-        const int vbytes = (int)(((int64_t)(rows - 1) * a.vs + D) * 2);
+        // rows <= 0 (a block past the sequence, loaded branch-free by the
+        // pipelined path) gives an empty resource: every lane reads zero
+        // (computed without branches, so the pipelined block stays one basic block)
+        const int rows = Lk - j;
+        const int rm1 = min(max(rows, 1), BN) - 1;
+        const int live = -(int)(rows > 0);
+        const int kbytes = (int)(((int64_t)rm1 * a.ks + D) * 2) & live;
+        const int vbytes = (int)(((int64_t)rm1 * a.vs + D) * 2) & live;
         const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(sv.k + (int64_t)j * a.ks * 2), (short)0, kbytes, kBufferDword3);
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
@@ -655,10 +718,12 @@ mfa_fwd16_kernel(KArgs a) {
                 o[qb - 1][db] = mfma16(vf[db][kb][st], __builtin_bit_cast(op_t, pw[qb - 1][kb][st]), o[qb - 1][db]);
             }
         };
+        if constexpr (MFA_SETPRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int s = 0; s < DS; ++s) sacc[0][kb] = mfma16(kf[kb][s], qf[0][s], sacc[0][kb]);
+        if constexpr (MFA_SETPRIO) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -670,7 +735,8 @@ mfa_fwd16_kernel(KArgs a) {
         for (int qb = 0; qb < QB; ++qb) {
             const int nm = (qb + 1 < QB ? kQK : 0) + (qb > 0 ? kPV : 0);
             qb_transform<NKB, BIAS, false>(a, sacc[qb], rs[qb], j, half);
-            float mpart = -INFINITY, alpha = 1.f, mu = 0.f;
+            float mpart[2] = {-INFINITY, -INFINITY}, alpha = 1.f, mu = 0.f;
+            float lacc[2] = {0.f, 0.f};
             bool moved = false;
 #pragma unroll
             for (int ci = 0; ci < NCH; ++ci) {
@@ -678,9 +744,13 @@ mfa_fwd16_kernel(KArgs a) {
                 for (int mi = ci * nm / NCH; mi < (ci + 1) * nm / NCH; ++mi) issue(qb, mi);
                 if (ci < NKB) {  // partial row max over key block ci
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) mpart = fmaxf(mpart, sacc[qb][ci][r]);
+                    for (int r = 0; r < 16; r += 2) {
+                        mpart[0] = fmaxf(mpart[0], sacc[qb][ci][r]);
+                        mpart[1] = fmaxf(mpart[1], sacc[qb][ci][r + 1]);
+                    }
                 } else if (ci == NKB) {  // merge halves, new running max
-                    moved = qb_update(rs[qb], max_halves(mpart), c, mu, alpha);
+                    moved = qb_update(rs[qb], max_halves(fmaxf(mpart[0], mpart[1])), c, mu, alpha);
+                    lacc[0] = rs[qb].l;
                 } else if (ci < NKB + 1 + DB) {  // rescale O rows (only if some row's max moved)
                     const int db = ci - NKB - 1;
                     if (moved) {
@@ -689,26 +759,27 @@ mfa_fwd16_kernel(KArgs a) {
                     }
                 } else {  // 8 probabilities of (kb, st)
                     const int g = ci - NKB - 1 - DB, kb = g / 2, st = g % 2;
-                    float acc = rs[qb].l;
 #pragma unroll
                     for (int w = 0; w < 4; ++w) {
                         const float p0 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w], c, -mu));
                         const float p1 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w + 1], c, -mu));
-                        pw[qb][kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, acc);
+                        pw[qb][kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, lacc[w & 1]);
                     }
-                    rs[qb].l = acc;
+                    if (ci == NCH - 1) rs[qb].l = lacc[0] + lacc[1];
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
         // last PV: the K/V staging of the next blocks (LDS stores, global
         // loads) is issued between its MFMAs, which then run underneath it
+        if constexpr (MFA_SETPRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int mi = 0; mi < kPV; ++mi) {
             issue(QB, mi);
             if (mi == 0) tail();
             __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (MFA_SETPRIO) __builtin_amdgcn_s_setprio(0);
     };
 
     // Block it is computed from LDS buffer it%2 while the registers hold
@@ -733,7 +804,16 @@ mfa_fwd16_kernel(KArgs a) {
         const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;  // row-major V
         if (QB >= 2 && MFA_PIPELINE && !skip && !masked) {
             if constexpr (QB >= 2 && MFA_PIPELINE) {
-                if constexpr (MFA_STAGE_IN_PV) {
+                if constexpr (MFA_STAGE_IN_PV && MFA_BRANCHFREE_STAGE) {
+                    // unconditional staging: no branch splits the pipelined
+                    // block, so no softmax work is sunk below the staging.
+                    // Past the last block it writes the idle buffer and loads
+                    // through an empty resource (no memory access).
+                    block_pipelined(kbuf, vtb, j, [&]() {
+                        swrite(buf ^ 1);
+                        gload(j + 2 * BN);
+                    });
+                } else if constexpr (MFA_STAGE_IN_PV) {
                     block_pipelined(kbuf, vtb, j, stage_next);
                 } else {
                     block_pipelined(kbuf, vtb, j, [] {});
@@ -752,6 +832,352 @@ mfa_fwd16_kernel(KArgs a) {
         __syncthreads();
     }
 
+    store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
+}
+
+// ----------------------------------------------------------------------------
+// 16-bit ping-pong kernel (head dims up to 64).
+//
+// Eight wavefronts in two groups of four, one wavefront of each group per
+// SIMD (grouped at start-up by the SIMD each one landed on).  Each wavefront
+// owns 64 query rows (two 32-query blocks) and alternates two phases:
+//   A(t): PV(t-1) then QK(t)        -- 32 MFMAs, no VALU work
+//   B(t): softmax of S(t)           -- VALU only
+// The groups run a phase apart, one workgroup barrier between phases, so on
+// every SIMD one wavefront keeps the matrix core busy while the other keeps the
+// vector ALU busy, and every operand a phase needs was produced by the phase
+// before it.  K/V tiles arrive by direct-to-LDS loads (one instruction
+// writes 64 x 16 bytes contiguously, lane i at 16*i, from a per-lane source
+// offset; no staging registers or LDS store instructions) into three stages
+// per operand: K(t) is read in both groups' A(t), V(t) in both groups'
+// A(t+1); each even phase 2u issues the loads of K(u+2) and V(u+1) into
+// stages the previous barrier released.  Tiles are unpadded with the 16-byte
+// chunks of each row XOR-swizzled, so the K operand reads (one row per lane)
+// and the transposed V reads (four rows per 16 lanes) are free of bank
+// conflicts.
+template <int DP, int NKB, bool IS_BF16, bool BIAS>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+mfa_fwd16_pp_kernel(KArgs a) {
+    constexpr int NW = 8;              // wavefronts
+    constexpr int NT = NW * 64;        // threads
+    constexpr int QB = 2;              // 32-query blocks per wavefront
+    constexpr int BM = NW * QB * 32;   // query rows per workgroup
+    constexpr int BN = NKB * 32;       // keys per K/V block
+    constexpr int DS = DP / 16;
+    constexpr int DB = DP / 32;
+    constexpr int NST = 3;             // LDS stages per operand
+    constexpr int CPR = DP / 8;        // 16-byte chunks per row
+    constexpr int TILE = BN * DP;      // elements of one K or V tile
+    constexpr int KV_ELEMS = 2 * NST * TILE;
+    constexpr int KST = DP + 8;        // Q staging row stride
+    constexpr int Q_ELEMS = BM * KST;
+    constexpr int SMEM = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+    constexpr int TI = BN * CPR / 64;  // 1 KiB wave loads per tile
+    static_assert(BN * CPR % 64 == 0 && TI <= NW, "one load per wavefront and tile at most");
+    typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
+
+    __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
+    __shared__ int simd_count[4];
+
+    int b, hq, tile;
+    if (!decode_tile(a, blockIdx.x, b, hq, tile)) return;
+    const SeqView sv = seq_view<2>(a, b, hq);
+    const int q0 = tile * BM;
+    if (q0 >= sv.Lq) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, half = lane >> 5;
+    const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
+    const int dq = Lk - Lq;
+
+    // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
+    if (tid < 4) simd_count[tid] = 0;
+    for (int c = tid; c < BM * CPR; c += NT) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        u32x4_t val = {0, 0, 0, 0};
+        if (q0 + row < Lq && col < D)
+            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 2);
+        *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
+    }
+    __syncthreads();
+    const int wq0 = q0 + wave * QB * 32;
+    op_t qf[QB][DS];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int s = 0; s < DS; ++s)
+            qf[qb][s] = *reinterpret_cast<const op_t*>(smem + (wave * QB * 32 + qb * 32 + l32) * KST + 16 * s + 8 * half);
+    // group: the order in which the wavefronts of one SIMD arrive (SIMD_ID =
+    // HW_ID[5:4]); the grouping only affects speed, never results
+    int arrival = 0;
+    if (lane == 0) arrival = atomicAdd(&simd_count[__builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4)], 1);
+    const int grp = __builtin_amdgcn_readfirstlane(arrival) & 1;
+    __syncthreads();
+
+    RowState rs[QB];
+    int lo_max[QB], hi_min[QB];  // per query block: largest lower / smallest upper key bound
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        rs[qb].center = wq0 + 32 * qb + l32 + dq;
+        rs[qb].lo = key_lo(a, rs[qb].center);
+        rs[qb].hi = key_hi(a, rs[qb].center, Lk);
+        rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+        rs[qb].m = -INFINITY;
+        rs[qb].l = 0.f;
+        const int r0 = wq0 + 32 * qb;
+        const int r1 = max(min(r0 + 31, Lq - 1), r0);
+        lo_max[qb] = key_lo(a, r1 + dq);
+        hi_min[qb] = key_hi(a, r0 + dq, Lk);
+    }
+    f32x16_t o[QB][DB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.f;
+    const float c = BIAS ? kLog2e : a.scale_log2;
+
+    // ---- key range of the workgroup
+    const int qlast = min(q0 + BM, Lq) - 1;
+    const int klo = key_lo(a, q0 + dq);
+    const int khi = key_hi(a, qlast + dq, Lk);
+    const int jbeg = (klo / BN) * BN;
+    const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
+    if (nblk == 0) {  // no valid key for any row of the tile: zeros
+        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
+        return;
+    }
+
+    // ---- LDS tiles: chunk c of row r is stored in chunk slot c ^ swz(r)
+    // K: the 8 lanes of one ds_read_b128 cycle read one chunk of 8 rows;
+    // V: the 16 lanes of one ds_read_b64_tr_b16 cycle read 2 chunks of 4 rows
+    constexpr int kSw8 = CPR % 8 == 0;  // 128-byte multiple rows (else 64 B)
+    auto kswz = [](int r) { return kSw8 ? (r & 7) : ((r >> 1) & 3); };
+    auto vswz = [](int r) { return kSw8 ? 2 * (r & 3) : 2 * ((r >> 1) & 1); };
+    uint16_t* const kst0 = smem;
+    uint16_t* const vst0 = smem + NST * TILE;
+    // direct-to-LDS loads: wave w fills tile slots 64*w .. 64*w+63 (w < TI)
+    const bool loader = wave < TI;
+    uint32_t kdoff = 0x80000000u, vdoff = 0x80000000u;
+    {
+        const int s = 64 * wave + lane;
+        const int r = s / CPR, p = s % CPR;
+        const int ck = p ^ kswz(r), cv = p ^ vswz(r);
+        if (loader && ck * 8 < D) kdoff = (uint32_t)(((int64_t)r * a.ks + ck * 8) * 2);
+        if (loader && cv * 8 < D) vdoff = (uint32_t)(((int64_t)r * a.vs + cv * 8) * 2);
+    }
+    // Buffer resource of K/V block u: base + j*stride bytes, sized to the
+    // block's valid rows (min(BN, Lk - j); none past the sequence).  All
+    // fields are wave-uniform and computed with scalar arithmetic (the
+    // host bounds the block span to 31 bits).
+    const int kfull = ((BN - 1) * (int)a.ks + D) * 2;
+    const int vfull = ((BN - 1) * (int)a.vs + D) * 2;
+    auto load_block = [&](const char* base, int64_t stride, int full, uint16_t* dst, uint32_t off, int u)
+        __attribute__((always_inline)) {
+        const int j = jbeg + u * BN;
+        const int rows = Lk - j;
+        int bytes = full;
+        if (rows < BN) bytes = rows > 0 ? ((rows - 1) * (int)stride + D) * 2 : 0;
+        lds_load16(reinterpret_cast<uint64_t>(base + (int64_t)j * stride * 2), (uint32_t)bytes, dst, off);
+    };
+    // loads of K block u into its stage u % NST (and likewise V); wave-uniform
+    auto load_k = [&](int u) __attribute__((always_inline)) {
+        if (loader) load_block(sv.k, a.ks, kfull, kst0 + (u % NST) * TILE + 512 * wave, kdoff, u);
+    };
+    auto load_v = [&](int u) __attribute__((always_inline)) {
+        if (loader) load_block(sv.v, a.vs, vfull, vst0 + (u % NST) * TILE + 512 * wave, vdoff, u);
+    };
+    // Barrier at the end of phase p, once this wave's LDS reads have returned
+    // and the loads the next phase reads have landed.  Phase p+1 reads the
+    // batch issued at phase p-3 (p odd) or p-4 (p even), so the newest one
+    // (p odd) or two (p even) batches of two loads may still be in flight.
+    auto phase_sync = [&](auto even_c) {
+        if constexpr (decltype(even_c)::value)
+            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+
+    // ---- MFMA operand reads.  K operand: row 32*kb + l32, chunk 2*s + half
+    // (rows 32*kb + l32 share the swizzle bits of l32).  PV A operand (V^T
+    // rows d = 32*db + lane%32, the 8 keys of accumulator registers
+    // 8*st..8*st+7) with two ds_read_b64_tr_b16: in each 16-lane group, lane
+    // i addresses 4 elements of key row (i/4) and lane j receives element j
+    // of rows 0..3.
+    const int kz = kswz(l32);
+    auto load_kf = [&](const uint16_t* kt, int kb, int s) -> op_t {
+        return *reinterpret_cast<const op_t*>(kt + (32 * kb + l32) * DP + 8 * ((2 * s + half) ^ kz));
+    };
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
+    const int tr_row = 4 * half + ((lane & 15) >> 2);
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int vz = vswz(tr_row);
+    auto load_vf = [&](const uint16_t* vt, int db, int kb, int st) -> op_t {
+        const uint16_t* p0 = vt + (32 * kb + 16 * st + tr_row) * DP + 8 * ((4 * db + (tr_col >> 3)) ^ vz) + (tr_col & 7);
+        const uint16_t* p1 = p0 + 8 * DP;
+        if constexpr (IS_BF16) {
+            typedef __attribute__((address_space(3))) bf16x4_t* lp;
+            const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p0));
+            const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p1));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+            typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+            typedef __attribute__((address_space(3))) fp16x4_t* lp;
+            const f16x4_t lo = __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p0)));
+            const f16x4_t hi = __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p1)));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+    auto mfma16 = [](const op_t& x, const op_t& y, const f32x16_t& acc) {
+        if constexpr (IS_BF16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, acc, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, acc, 0, 0, 0);
+    };
+
+    f32x16_t sacc[QB][NKB];  // S^T(t) of query block qb
+    u32x4_t pw[QB][NKB][2];  // 16-bit P^T(t), PV B operands
+
+    // A(u): PV(u-1) then QK(u).  Step i reads one K or V
+    // fragment, which feeds both query blocks; fragments are read
+    // MFA_PP_AHEAD steps ahead of their MFMAs (sched_barrier keeps the
+    // compiler from hoisting every read to the top).
+    auto phase_a = [&](int u) __attribute__((always_inline)) {
+        constexpr int NPV = DB * NKB * 2;
+        constexpr int NQK = NKB * DS;
+        constexpr int NS = NPV + NQK;
+        constexpr int AH = MFA_PP_AHEAD;
+        const uint16_t* vt = vst0 + ((u + NST - 1) % NST) * TILE;
+        const uint16_t* kt = kst0 + (u % NST) * TILE;
+        op_t fr[AH + 1];
+        auto load_step = [&](int i) __attribute__((always_inline)) {
+            if (i < NPV) {
+                const int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
+                fr[i % (AH + 1)] = load_vf(vt, db, kb, st);
+            } else {
+                const int m = i - NPV, kb = m % NKB, s = m / NKB;
+                fr[i % (AH + 1)] = load_kf(kt, kb, s);
+            }
+        };
+        auto mfma_step = [&](int i) __attribute__((always_inline)) {
+            const op_t f = fr[i % (AH + 1)];
+            if (i < NPV) {
+                const int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    o[qb][db] = mfma16(f, __builtin_bit_cast(op_t, pw[qb][kb][st]), o[qb][db]);
+            } else {
+                const int m = i - NPV, kb = m % NKB, s = m / NKB;
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    sacc[qb][kb] = mfma16(f, qf[qb][s], s == 0 ? f32x16_t{} : sacc[qb][kb]);
+            }
+        };
+        if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(MFA_PP_PRIO);
+#pragma unroll
+        for (int i = 0; i < AH && i < NS; ++i) load_step(i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            if (i + AH < NS) load_step(i + AH);
+            mfma_step(i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(0);
+    };
+    // B(u): online softmax of S(u) for both query blocks
+    auto phase_b = [&](int u) __attribute__((always_inline)) {
+        const int j = jbeg + u * BN;
+        // the softmax stays between the barriers: it starts from S as the
+        // phase begins and its P is complete before the phase ends
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) pin(sacc[qb][kb]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            if ((j >= lo_max[qb]) && (j + BN - 1 <= hi_min[qb]))
+                qb_transform<NKB, BIAS, false>(a, sacc[qb], rs[qb], j, half);
+            else
+                qb_transform<NKB, BIAS, true>(a, sacc[qb], rs[qb], j, half);
+        }
+        // both query blocks' max, update and probabilities in one branch-free
+        // stretch (independent chains for the scheduler to interleave); the
+        // rare rescale of O follows (O is next read by PV in the next phase)
+        float mx[QB], mu[QB], alpha[QB];
+        bool moved[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) mx[qb] = qb_max<NKB>(sacc[qb]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_update_flat(rs[qb], mx[qb], c, mu[qb], alpha[qb]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu[qb], c);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+            if (moved[qb]) scale_rows<DB>(o[qb], alpha[qb]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) pin(pw[qb][kb][st]);
+    };
+    // ---- prologue: K(0), K(1), V(0) resident.  A(0) runs PV(-1) with P = 0
+    // against the zeroed V stage of block -1; A(n) runs a QK of block n whose
+    // result is never used.  (One instance of each phase.)
+    for (int c2 = tid; c2 < TILE / 8; c2 += NT)
+        *reinterpret_cast<u32x4_t*>(vst0 + (NST - 1) * TILE + 8 * c2) = u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int st = 0; st < 2; ++st) pw[qb][kb][st] = u32x4_t{0, 0, 0, 0};
+    load_k(0);
+    load_k(1);
+    load_v(0);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- phases: group 0 runs A(0) B(0) A(1) ... B(n-1) A(n) at phases
+    // 0..2n, group 1 the same at phases 1..2n+1; every wave issues the loads
+    // of K(u+2), V(u+1) at phase 2u (blocks past the end read zero).
+    auto dma = [&](int u) __attribute__((always_inline)) {
+        load_k(u + 2);
+        load_v(u + 1);
+    };
+    using EVEN = std::true_type;
+    using ODD = std::false_type;
+    auto run = [&](auto grp_c) __attribute__((always_inline)) {
+        constexpr int G = decltype(grp_c)::value;
+        if constexpr (G == 1) {
+            dma(0);
+            phase_sync(EVEN{});  // phase 0 (idle)
+        }
+        for (int u = 0; u < nblk; ++u) {
+            if constexpr (G == 0) dma(u);
+            phase_a(u);
+            if constexpr (G == 0) phase_sync(EVEN{}); else phase_sync(ODD{});
+            if constexpr (G == 1) dma(u + 1);
+            phase_b(u);
+            if constexpr (G == 0) phase_sync(ODD{}); else phase_sync(EVEN{});
+        }
+        if constexpr (G == 0) dma(nblk);
+        phase_a(nblk);
+        if constexpr (G == 0) {
+            phase_sync(EVEN{});  // phase 2n
+            phase_sync(ODD{});   // phase 2n+1 (idle)
+        } else {
+            phase_sync(ODD{});   // phase 2n+1
+        }
+    };
+    if (grp == 0)
+        run(std::integral_constant<int, 0>{});
+    else
+        run(std::integral_constant<int, 1>{});
+    // no direct-to-LDS write may land after the workgroup's LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
 }
 
@@ -942,6 +1368,7 @@ struct KernelCfg {
     int keys;  // keys per K/V block
     int lds;   // LDS bytes
     const char* name;
+    int threads = kThreads;  // threads per workgroup
 };
 
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
@@ -949,6 +1376,12 @@ KernelCfg cfg16(const char* name) {
     constexpr int BM = kWaves * QB * 32, BN = NKB * 32;
     constexpr int kv = 2 * (BN * (DP + 8) + BN * (DP + MFA_V_PAD)), qs = BM * (DP + 8);
     return KernelCfg{mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs), name};
+}
+template <int DP, int NKB, bool IS_BF16, bool BIAS>
+KernelCfg cfg16pp(const char* name) {
+    constexpr int BM = 8 * 2 * 32, BN = NKB * 32;
+    constexpr int kv = 2 * 3 * BN * DP, qs = BM * (DP + 8);  // three K and three V stages / Q staging
+    return KernelCfg{mfa_fwd16_pp_kernel<DP, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs) + 16, name, 512};
 }
 template <int DP, int NKB, bool BIAS>
 KernelCfg cfg32(const char* name) {
@@ -975,8 +1408,17 @@ KernelCfg cfg32(const char* name) {
 #define MFA_STR2(...) #__VA_ARGS__
 #define MFA_STR(...) MFA_STR2(__VA_ARGS__)
 
+// head dims up to 64 use the ping-pong kernel (8 wavefronts, 512-row tiles)
+#ifndef MFA_PINGPONG
+#define MFA_PINGPONG 1
+#endif
 template <bool IS_BF16, bool BIAS>
-KernelCfg select16(int dp) {
+KernelCfg select16(int dp, bool fills_chip) {
+    if (MFA_PINGPONG && dp <= 64 && fills_chip) {
+        if (dp == 32)
+            return cfg16pp<32, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,2,2>" : "mfa_fwd16pp<f16,d32,2,2>");
+        return cfg16pp<64, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,2,2>" : "mfa_fwd16pp<f16,d64,2,2>");
+    }
     switch (dp) {
         case 32: return cfg16<32, MFA_D32_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32," MFA_STR(MFA_D32_TILE) ">" : "mfa_fwd16<f16,d32," MFA_STR(MFA_D32_TILE) ">");
         case 64: return cfg16<64, MFA_D64_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64," MFA_STR(MFA_D64_TILE) ">" : "mfa_fwd16<f16,d64," MFA_STR(MFA_D64_TILE) ">");
@@ -1049,14 +1491,28 @@ int make_plan(const mfa_fwd_params* p, Plan* plan) {
             return set_err(MFA_ERR_INVALID, "mfa_fwd: alibi_batch_stride must be 0 or heads_q");
     }
 
+    // K/V blocks are addressed with 32-bit byte offsets from the block start
+    const int64_t kv_span = (int64_t)63 * (p->k_seq_stride > p->v_seq_stride ? p->k_seq_stride : p->v_seq_stride);
+    if (p->k_seq_stride < 0 || p->v_seq_stride < 0 || (kv_span + D) * es >= ((int64_t)1 << 31))
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: k/v sequence strides must be >= 0 and span < 2 GiB per 64 rows");
+
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128;
     const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);
+    // the 512-row ping-pong tiles are used when they still give every CU a
+    // workgroup (256 CUs on MI355X)
+    if (p->tile_hint < MFA_TILE_AUTO || p->tile_hint > MFA_TILE_PINGPONG)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: unknown tile_hint %d", p->tile_hint);
+    if (p->tile_hint == MFA_TILE_PINGPONG && (din == MFA_DTYPE_F32 || dp > 64))
+        return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles need bf16/fp16 and head_dim <= 64");
+    const bool fills_chip = p->tile_hint == MFA_TILE_AUTO
+                                ? (int64_t)p->batch * p->heads_q * ((p->seqlen_q + 511) / 512) >= 256
+                                : p->tile_hint == MFA_TILE_PINGPONG;
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp) : select32<false>(dp);
     else if (din == MFA_DTYPE_BF16)
-        plan->cfg = bias ? select16<true, true>(dp) : select16<true, false>(dp);
+        plan->cfg = bias ? select16<true, true>(dp, fills_chip) : select16<true, false>(dp, fills_chip);
     else
-        plan->cfg = bias ? select16<false, true>(dp) : select16<false, false>(dp);
+        plan->cfg = bias ? select16<false, true>(dp, fills_chip) : select16<false, false>(dp, fills_chip);
 
     KArgs& a = plan->args;
     memset(&a, 0, sizeof(a));
@@ -1125,7 +1581,7 @@ int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info) {
     const int rc = make_plan(params, &plan);
     if (rc != MFA_OK) return rc;
     info->grid_x = plan.empty ? 0 : plan.grid;
-    info->block_x = kThreads;
+    info->block_x = plan.cfg.threads;
     info->rows_per_block = plan.cfg.rows;
     info->keys_per_block = plan.cfg.keys;
     info->lds_bytes = plan.cfg.lds;
@@ -1140,7 +1596,7 @@ int mfa_fwd(const mfa_fwd_params* params, void* stream) {
     const int rc = make_plan(params, &plan);
     if (rc != MFA_OK) return rc;
     if (plan.empty) return MFA_OK;
-    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), plan.args);
+    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, static_cast<hipStream_t>(stream), plan.args);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd: launch failed: %s", hipGetErrorString(e));
     return MFA_OK;

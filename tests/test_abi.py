@@ -46,7 +46,8 @@ def test_abi_version_and_struct_size(lib):
     assert lib.mfa_params_size() == ctypes.sizeof(_hip.MfaFwdParams)
     src = open(HEADER).read()
     assert f"#define MFA_ABI_VERSION {_hip.MFA_ABI_VERSION}" in src
-    for name in ("MFA_DTYPE_F16", "MFA_DTYPE_BF16", "MFA_DTYPE_F32", "MFA_ERR_INVALID", "MFA_ERR_UNSUPPORTED"):
+    for name in ("MFA_DTYPE_F16", "MFA_DTYPE_BF16", "MFA_DTYPE_F32", "MFA_ERR_INVALID", "MFA_ERR_UNSUPPORTED",
+                 "MFA_TILE_AUTO", "MFA_TILE_256", "MFA_TILE_PINGPONG"):
         val = int(re.search(rf"#define {name} (-?\d+)", src).group(1))
         assert val == getattr(_hip, name)
 
@@ -84,6 +85,12 @@ def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
     (lambda p: setattr(p, "k_seq_stride", 68), _hip.MFA_ERR_INVALID, "strides"),
     (lambda p: setattr(p, "o", None), _hip.MFA_ERR_INVALID, "NULL"),
     (lambda p: setattr(p, "cu_seqlens_q", 256), _hip.MFA_ERR_INVALID, "cu_seqlens"),
+    (lambda p: setattr(p, "tile_hint", 3), _hip.MFA_ERR_INVALID, "tile_hint"),
+    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "dtype_in", _hip.MFA_DTYPE_F32),
+                setattr(p, "dtype_out", _hip.MFA_DTYPE_F32)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
+    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "head_dim", 128),
+                setattr(p, "q_head_stride", 128)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
+    (lambda p: setattr(p, "k_seq_stride", -64), _hip.MFA_ERR_INVALID, "sequence strides"),
     (lambda p: setattr(p, "seqlen_k", -1), _hip.MFA_ERR_INVALID, "negative"),
 ])
 def test_invalid_requests_are_rejected_before_launch(lib, mutate, code, msg):
@@ -112,10 +119,22 @@ def test_empty_problem_is_a_no_op(lib):
 def test_launch_geometry_of_the_baseline_configs(lib):
     bf = torch.empty(1, 8192, 16, 64, dtype=torch.bfloat16)
     info = _kernel.launch_info(bf, bf, bf)
-    assert info.block_x == 256 and info.grid_x * info.rows_per_block >= 8192 * 16
-    assert info.kernel_name.startswith(b"mfa_fwd16<bf16,d64")
+    # config 2 fills the chip with 512-row ping-pong tiles (8 wavefronts)
+    assert info.block_x == 512 and info.grid_x * info.rows_per_block >= 8192 * 16
+    assert info.kernel_name.startswith(b"mfa_fwd16pp<bf16,d64")
     # XCD-grouped schedule: grid is a multiple of 8 and covers every (head, tile)
     assert info.grid_x % 8 == 0
+    # too few 512-row tiles for 256 CUs: the 256-row kernel
+    small = torch.empty(1, 2048, 16, 64, dtype=torch.bfloat16)
+    info = _kernel.launch_info(small, small, small)
+    assert info.block_x == 256 and info.kernel_name.startswith(b"mfa_fwd16<bf16,d64")
+    # the tile hint overrides the automatic choice
+    p = good_params(L=2048, H=16)
+    p.tile_hint = _hip.MFA_TILE_PINGPONG
+    li = _hip.launch_info(p)
+    assert li.block_x == 512 and li.rows_per_block == 512
+    p.tile_hint = _hip.MFA_TILE_256
+    assert _hip.launch_info(p).block_x == 256
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
     info = _kernel.launch_info(f16, f16, f16, causal=True)
     assert info.kernel_name.startswith(b"mfa_fwd16<f16,d128")

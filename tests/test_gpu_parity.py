@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import mtlflashattn_amd as mfa
-from mtlflashattn_amd import _kernel
+from mtlflashattn_amd import _hip, _kernel
 from oracle import chunked
 from gpu_util import (
     assert_output, assert_parity, default_scale, make_qkv, make_varlen, max_err, native_library_mapped,
@@ -18,6 +18,14 @@ from gpu_util import (
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+@pytest.fixture(params=[_hip.MFA_TILE_256, _hip.MFA_TILE_PINGPONG], ids=["tile256", "pingpong"])
+def tile(request, monkeypatch):
+    """Run a test through each bf16/fp16 kernel: 256-row tiles and the 512-row
+    ping-pong tiles (head dims <= 64; other cases keep the library's choice)."""
+    monkeypatch.setattr(_kernel, "_TILE_HINT", request.param)
+    return request.param
 
 
 def run_both(q, k, v, **kw):
@@ -56,6 +64,7 @@ def test_config1_fp32_exact_inputs():
     print(f"config1 fp32 max abs err {e32:.3e}")
 
 
+@pytest.mark.usefixtures("tile")
 class TestFlashAttnFunc:
     @pytest.mark.parametrize("dtype", DTYPES)
     def test_mha_self_attn(self, dtype):
@@ -118,6 +127,7 @@ class TestFlashAttnFunc:
         check(q, q, q, "transposed view")
 
 
+@pytest.mark.usefixtures("tile")
 class TestFeatures:
     @pytest.mark.parametrize("dtype", DTYPES)
     def test_softcap(self, dtype):
@@ -158,6 +168,7 @@ class TestFeatures:
             mfa.flash_attn_func(q, k, v, alibi_slopes=torch.ones(3, device="cuda"))
 
 
+@pytest.mark.usefixtures("tile")
 class TestVarlen:
     def check_varlen(self, seqlens_q, seqlens_k, Hq=4, Hkv=4, D=64, dtype=torch.float32, causal=False,
                      alibi=None, **kw):
@@ -217,6 +228,7 @@ class TestVarlen:
             mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k_bad, 32, 64)
 
 
+@pytest.mark.usefixtures("tile")
 class TestPacked:
     def test_qkvpacked_matches_unpacked(self):
         g = torch.Generator().manual_seed(0)
