@@ -44,8 +44,8 @@ _warned_modes = set()
 
 
 # Preferred C-ABI tile_hint for bf16/fp16 launches (0 = the library's choice);
-# tests set it to run every case through each kernel.  A preference the
-# launch cannot take (fp32, ping-pong with head_dim > 64) falls back to 0.
+# tests set it to run every case through each kernel.  A preference the launch
+# cannot take (fp32, ping-pong with a head dim above 64) falls back to 0.
 _TILE_HINT = 0
 
 

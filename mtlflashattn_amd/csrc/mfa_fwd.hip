@@ -86,6 +86,10 @@ constexpr int kWaves = 4;
 #ifndef MFA_PP_AHEAD
 #define MFA_PP_AHEAD 2
 #endif
+// the same for one query block per wavefront (one MFMA per fragment)
+#ifndef MFA_PP_AHEAD1
+#define MFA_PP_AHEAD1 4
+#endif
 // raise the wave priority during the MFMA phase of the ping-pong kernel
 #ifndef MFA_PP_PRIO
 #define MFA_PP_PRIO 1
@@ -836,12 +840,13 @@ mfa_fwd16_kernel(KArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// 16-bit ping-pong kernel (head dims up to 64).
+// 16-bit ping-pong kernel.
 //
 // Eight wavefronts in two groups of four, one wavefront of each group per
 // SIMD (grouped at start-up by the SIMD each one landed on).  Each wavefront
-// owns 64 query rows (two 32-query blocks) and alternates two phases:
-//   A(t): PV(t-1) then QK(t)        -- 32 MFMAs, no VALU work
+// owns QB 32-query blocks (two for head dims up to 64, one above) and
+// alternates two phases:
+//   A(t): PV(t-1) then QK(t)        -- MFMAs only (32 for d64 x2, d128 x1)
 //   B(t): softmax of S(t)           -- VALU only
 // The groups run a phase apart, one workgroup barrier between phases, so on
 // every SIMD one wavefront keeps the matrix core busy while the other keeps the
@@ -855,12 +860,11 @@ mfa_fwd16_kernel(KArgs a) {
 // chunks of each row XOR-swizzled, so the K operand reads (one row per lane)
 // and the transposed V reads (four rows per 16 lanes) are free of bank
 // conflicts.
-template <int DP, int NKB, bool IS_BF16, bool BIAS>
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 mfa_fwd16_pp_kernel(KArgs a) {
     constexpr int NW = 8;              // wavefronts
     constexpr int NT = NW * 64;        // threads
-    constexpr int QB = 2;              // 32-query blocks per wavefront
     constexpr int BM = NW * QB * 32;   // query rows per workgroup
     constexpr int BN = NKB * 32;       // keys per K/V block
     constexpr int DS = DP / 16;
@@ -873,7 +877,9 @@ mfa_fwd16_pp_kernel(KArgs a) {
     constexpr int Q_ELEMS = BM * KST;
     constexpr int SMEM = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
     constexpr int TI = BN * CPR / 64;  // 1 KiB wave loads per tile
-    static_assert(BN * CPR % 64 == 0 && TI <= NW, "one load per wavefront and tile at most");
+    // every loading wavefront issues NL loads per tile (waves >= TI none)
+    constexpr int NL = TI >= NW ? TI / NW : 1;
+    static_assert(BN * CPR % 64 == 0 && (TI < NW || TI % NW == 0), "equal load counts per wavefront");
     typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
 
     __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
@@ -957,15 +963,17 @@ mfa_fwd16_pp_kernel(KArgs a) {
     auto vswz = [](int r) { return kSw8 ? 2 * (r & 3) : 2 * ((r >> 1) & 1); };
     uint16_t* const kst0 = smem;
     uint16_t* const vst0 = smem + NST * TILE;
-    // direct-to-LDS loads: wave w fills tile slots 64*w .. 64*w+63 (w < TI)
-    const bool loader = wave < TI;
-    uint32_t kdoff = 0x80000000u, vdoff = 0x80000000u;
-    {
-        const int s = 64 * wave + lane;
+    // direct-to-LDS loads: load i of wave w fills tile slots
+    // 64*(w + NW*i) .. +63 (w < TI when a tile is smaller than NW loads)
+    const bool loader = TI >= NW || wave < TI;
+    uint32_t kdoff[NL], vdoff[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int s = 64 * (wave + NW * i) + lane;
         const int r = s / CPR, p = s % CPR;
         const int ck = p ^ kswz(r), cv = p ^ vswz(r);
-        if (loader && ck * 8 < D) kdoff = (uint32_t)(((int64_t)r * a.ks + ck * 8) * 2);
-        if (loader && cv * 8 < D) vdoff = (uint32_t)(((int64_t)r * a.vs + cv * 8) * 2);
+        kdoff[i] = loader && ck * 8 < D ? (uint32_t)(((int64_t)r * a.ks + ck * 8) * 2) : 0x80000000u;
+        vdoff[i] = loader && cv * 8 < D ? (uint32_t)(((int64_t)r * a.vs + cv * 8) * 2) : 0x80000000u;
     }
     // Buffer resource of K/V block u: base + j*stride bytes, sized to the
     // block's valid rows (min(BN, Lk - j); none past the sequence).  All
@@ -983,20 +991,28 @@ mfa_fwd16_pp_kernel(KArgs a) {
     };
     // loads of K block u into its stage u % NST (and likewise V); wave-uniform
     auto load_k = [&](int u) __attribute__((always_inline)) {
-        if (loader) load_block(sv.k, a.ks, kfull, kst0 + (u % NST) * TILE + 512 * wave, kdoff, u);
+        if (loader) {
+#pragma unroll
+            for (int i = 0; i < NL; ++i)
+                load_block(sv.k, a.ks, kfull, kst0 + (u % NST) * TILE + 512 * (wave + NW * i), kdoff[i], u);
+        }
     };
     auto load_v = [&](int u) __attribute__((always_inline)) {
-        if (loader) load_block(sv.v, a.vs, vfull, vst0 + (u % NST) * TILE + 512 * wave, vdoff, u);
+        if (loader) {
+#pragma unroll
+            for (int i = 0; i < NL; ++i)
+                load_block(sv.v, a.vs, vfull, vst0 + (u % NST) * TILE + 512 * (wave + NW * i), vdoff[i], u);
+        }
     };
     // Barrier at the end of phase p, once this wave's LDS reads have returned
     // and the loads the next phase reads have landed.  Phase p+1 reads the
     // batch issued at phase p-3 (p odd) or p-4 (p even), so the newest one
-    // (p odd) or two (p even) batches of two loads may still be in flight.
+    // (p odd) or two (p even) batches of 2*NL loads may still be in flight.
     auto phase_sync = [&](auto even_c) {
         if constexpr (decltype(even_c)::value)
-            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(4 * NL) : "memory");
         else
-            asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * NL) : "memory");
     };
 
     // ---- MFMA operand reads.  K operand: row 32*kb + l32, chunk 2*s + half
@@ -1048,7 +1064,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
         constexpr int NPV = DB * NKB * 2;
         constexpr int NQK = NKB * DS;
         constexpr int NS = NPV + NQK;
-        constexpr int AH = MFA_PP_AHEAD;
+        constexpr int AH = QB == 1 ? MFA_PP_AHEAD1 : MFA_PP_AHEAD;
         const uint16_t* vt = vst0 + ((u + NST - 1) % NST) * TILE;
         const uint16_t* kt = kst0 + (u % NST) * TILE;
         op_t fr[AH + 1];
@@ -1377,11 +1393,12 @@ KernelCfg cfg16(const char* name) {
     constexpr int kv = 2 * (BN * (DP + 8) + BN * (DP + MFA_V_PAD)), qs = BM * (DP + 8);
     return KernelCfg{mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs), name};
 }
-template <int DP, int NKB, bool IS_BF16, bool BIAS>
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
 KernelCfg cfg16pp(const char* name) {
-    constexpr int BM = 8 * 2 * 32, BN = NKB * 32;
+    constexpr int BM = 8 * QB * 32, BN = NKB * 32;
     constexpr int kv = 2 * 3 * BN * DP, qs = BM * (DP + 8);  // three K and three V stages / Q staging
-    return KernelCfg{mfa_fwd16_pp_kernel<DP, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs) + 16, name, 512};
+    return KernelCfg{mfa_fwd16_pp_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs) + 16, name,
+                     512};
 }
 template <int DP, int NKB, bool BIAS>
 KernelCfg cfg32(const char* name) {
@@ -1408,16 +1425,20 @@ KernelCfg cfg32(const char* name) {
 #define MFA_STR2(...) #__VA_ARGS__
 #define MFA_STR(...) MFA_STR2(__VA_ARGS__)
 
-// head dims up to 64 use the ping-pong kernel (8 wavefronts, 512-row tiles)
+// bf16/fp16 head dims up to 64 use the ping-pong kernel (8 wavefronts,
+// 512-row tiles) when its tiles fill the chip.  (With one 32-query block per
+// wavefront, as a 128-wide head dim allows at two wavefronts per SIMD, every
+// K/V fragment feeds one MFMA and LDS bandwidth binds: measured slower than
+// the 4-wavefront kernel on the d128 configurations.)
 #ifndef MFA_PINGPONG
 #define MFA_PINGPONG 1
 #endif
 template <bool IS_BF16, bool BIAS>
 KernelCfg select16(int dp, bool fills_chip) {
-    if (MFA_PINGPONG && dp <= 64 && fills_chip) {
+    if (MFA_PINGPONG && fills_chip && dp <= 64) {
         if (dp == 32)
-            return cfg16pp<32, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,2,2>" : "mfa_fwd16pp<f16,d32,2,2>");
-        return cfg16pp<64, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,2,2>" : "mfa_fwd16pp<f16,d64,2,2>");
+            return cfg16pp<32, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,2,2>" : "mfa_fwd16pp<f16,d32,2,2>");
+        return cfg16pp<64, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,2,2>" : "mfa_fwd16pp<f16,d64,2,2>");
     }
     switch (dp) {
         case 32: return cfg16<32, MFA_D32_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32," MFA_STR(MFA_D32_TILE) ">" : "mfa_fwd16<f16,d32," MFA_STR(MFA_D32_TILE) ">");
