@@ -45,6 +45,7 @@
 #include <string.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "mfa.h"
 
@@ -162,6 +163,34 @@ __device__ __forceinline__ void lds_load16(uint64_t base, uint32_t bytes, uint16
                  :
                  : "s"(m0), "v"(off), "s"(r)
                  : "memory", "m0");
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0 .. N-1.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// ds_read_b64_tr_b16 at LDS byte address addr + OFF, issued from inline asm
+// so the constant lands in the offset field.  The compiler does not track
+// this load: the caller waits (lds_wait) before touching the result.
+template <int OFF>
+__device__ __forceinline__ u32x2_t lds_read_tr16(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "DS offset field");
+    u32x2_t r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+// Wait until at most N LDS operations are in flight; x and y (results of
+// asynchronous LDS reads) are tied through the wait, so nothing reads or moves
+// them before it.
+template <int N, class T>
+__device__ __forceinline__ void lds_wait(T& x, T& y) {
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
 }
 
 // Empty asm that reads and rewrites x in registers: pure arithmetic can be
@@ -362,14 +391,15 @@ __device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float
 }
 
 // qb_update without a branch: the same result, with the rescale of O left
-// to the caller (needed exactly when it returns true).
+// to the caller, by `alpha`, exactly when it returns true.  (alpha is not
+// forced to 1 otherwise, so the caller's conditional rescale cannot be
+// turned into an unconditional multiply by 1.)
 __device__ __forceinline__ bool qb_update_flat(RowState& rs, float mx, float c, float& mu, float& alpha) {
     const bool moved = __any((mx - rs.m) * c > (float)MFA_RESCALE_TAU);
     const float mn = fmaxf(rs.m, mx);
-    const float a_ = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
-    alpha = moved ? a_ : 1.f;
+    alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
     rs.m = moved ? mn : rs.m;
-    rs.l *= alpha;
+    rs.l *= moved ? alpha : 1.f;
     mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
     return moved;
 }
@@ -1021,31 +1051,22 @@ mfa_fwd16_pp_kernel(KArgs a) {
     // 8*st..8*st+7) with two ds_read_b64_tr_b16: in each 16-lane group, lane
     // i addresses 4 elements of key row (i/4) and lane j receives element j
     // of rows 0..3.
+    // Per-lane element offsets, swizzle included, of the fragments that differ
+    // only in their lane part: K step s, V head-dim block db.  The key-block
+    // and row-group parts are compile-time constants (immediate offsets).
     const int kz = kswz(l32);
-    auto load_kf = [&](const uint16_t* kt, int kb, int s) -> op_t {
-        return *reinterpret_cast<const op_t*>(kt + (32 * kb + l32) * DP + 8 * ((2 * s + half) ^ kz));
+    int klane[DS];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) klane[s] = l32 * DP + 8 * ((2 * s + half) ^ kz);
+    auto load_kf = [&](const uint16_t* const (&kp)[DS], int kb, int s) -> op_t {
+        return *reinterpret_cast<const op_t*>(kp[s] + 32 * kb * DP);
     };
-    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
-    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
     const int tr_row = 4 * half + ((lane & 15) >> 2);
     const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     const int vz = vswz(tr_row);
-    auto load_vf = [&](const uint16_t* vt, int db, int kb, int st) -> op_t {
-        const uint16_t* p0 = vt + (32 * kb + 16 * st + tr_row) * DP + 8 * ((4 * db + (tr_col >> 3)) ^ vz) + (tr_col & 7);
-        const uint16_t* p1 = p0 + 8 * DP;
-        if constexpr (IS_BF16) {
-            typedef __attribute__((address_space(3))) bf16x4_t* lp;
-            const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p0));
-            const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p1));
-            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        } else {
-            typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
-            typedef __attribute__((address_space(3))) fp16x4_t* lp;
-            const f16x4_t lo = __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p0)));
-            const f16x4_t hi = __builtin_bit_cast(f16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p1)));
-            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        }
-    };
+    int vlane[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) vlane[db] = tr_row * DP + 8 * ((4 * db + (tr_col >> 3)) ^ vz) + (tr_col & 7);
     auto mfma16 = [](const op_t& x, const op_t& y, const f32x16_t& acc) {
         if constexpr (IS_BF16)
             return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, acc, 0, 0, 0);
@@ -1067,40 +1088,63 @@ mfa_fwd16_pp_kernel(KArgs a) {
         constexpr int AH = QB == 1 ? MFA_PP_AHEAD1 : MFA_PP_AHEAD;
         const uint16_t* vt = vst0 + ((u + NST - 1) % NST) * TILE;
         const uint16_t* kt = kst0 + (u % NST) * TILE;
-        op_t fr[AH + 1];
-        auto load_step = [&](int i) __attribute__((always_inline)) {
-            if (i < NPV) {
-                const int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
-                fr[i % (AH + 1)] = load_vf(vt, db, kb, st);
-            } else {
-                const int m = i - NPV, kb = m % NKB, s = m / NKB;
-                fr[i % (AH + 1)] = load_kf(kt, kb, s);
+        const uint16_t* kp[DS];
+        uint32_t vp[DB];
+#pragma unroll
+        for (int s = 0; s < DS; ++s) kp[s] = kt + klane[s];
+        const uint32_t vt_lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vt;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) vp[db] = vt_lds + 2 * vlane[db];
+        // step i: one V fragment (two transposed reads, issued from asm with
+        // the row-group offset as an immediate) or one K fragment (compiler
+        // load); fragments are read AH steps ahead of their MFMAs
+        u32x2_t vlo[AH + 1], vhi[AH + 1];
+        op_t kfr[AH + 1];
+        auto load_step = [&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            if constexpr (i < NPV) {
+                constexpr int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
+                constexpr int off = (32 * kb + 16 * st) * DP * 2;
+                vlo[i % (AH + 1)] = lds_read_tr16<off>(vp[db]);
+                vhi[i % (AH + 1)] = lds_read_tr16<off + 8 * DP * 2>(vp[db]);
+            } else if constexpr (i < NS) {
+                constexpr int m = i - NPV, kb = m % NKB, s = m / NKB;
+                kfr[i % (AH + 1)] = load_kf(kp, kb, s);
             }
         };
-        auto mfma_step = [&](int i) __attribute__((always_inline)) {
-            const op_t f = fr[i % (AH + 1)];
-            if (i < NPV) {
-                const int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
+        auto mfma_step = [&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            if constexpr (i < NPV) {
+                // LDS operations issued after this step's reads (steps i+1 .. i+AH)
+                constexpr int after = [] {
+                    int n = 0;
+                    for (int k = i + 1; k <= i + AH && k < NS; ++k) n += k < NPV ? 2 : 1;
+                    return n;
+                }();
+                u32x2_t lo = vlo[i % (AH + 1)], hi = vhi[i % (AH + 1)];
+                lds_wait<after>(lo, hi);
+                const op_t f = __builtin_bit_cast(op_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+                constexpr int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
                     o[qb][db] = mfma16(f, __builtin_bit_cast(op_t, pw[qb][kb][st]), o[qb][db]);
             } else {
-                const int m = i - NPV, kb = m % NKB, s = m / NKB;
+                const op_t f = kfr[i % (AH + 1)];
+                constexpr int m = i - NPV, kb = m % NKB, s = m / NKB;
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
                     sacc[qb][kb] = mfma16(f, qf[qb][s], s == 0 ? f32x16_t{} : sacc[qb][kb]);
             }
         };
         if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(MFA_PP_PRIO);
-#pragma unroll
-        for (int i = 0; i < AH && i < NS; ++i) load_step(i);
+        static_for<AH>(load_step);
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < NS; ++i) {
-            if (i + AH < NS) load_step(i + AH);
-            mfma_step(i);
+        static_for<NS>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            load_step(std::integral_constant<int, i + AH>{});
+            mfma_step(ic);
             __builtin_amdgcn_sched_barrier(0);
-        }
+        });
         if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(0);
     };
     // B(u): online softmax of S(u) for both query blocks
