@@ -343,9 +343,13 @@ __device__ __forceinline__ void qb_transform(const KArgs& a, f32x16_t (&s)[NKB],
         }
     }
     if constexpr (MASKED) {
+        // (the pinned copy keeps the compiler from hoisting the 32 key
+        // indices out of the masked path into every block)
+        int jm = j;
+        asm volatile("" : "+v"(jm));
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-            const int kbase = j + 32 * kb + 4 * half;
+            const int kbase = jm + 32 * kb + 4 * half;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = kbase + acc_row(r);
@@ -1177,6 +1181,9 @@ mfa_fwd16_pp_kernel(KArgs a) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
             if (moved[qb]) scale_rows<DB>(o[qb], alpha[qb]);
+        // (the row sums stay in this phase too)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) pin(rs[qb].l);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
