@@ -14,7 +14,8 @@ Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
   cpu_baseline : the reference's chunked-fp32 torch path (oracle/chunked.py)
                  timed on this host's cores on a bounded sample of the same
                  workload (a subset of heads).
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7]
+(6 and 7: HBM-bound short-L shapes, roofline in GB/s against 8 TB/s)
 """
 from __future__ import annotations
 
@@ -31,6 +32,7 @@ if REPO not in sys.path:
 
 METRIC = "attn fwd effective TFLOP/s + % MFMA peak, bf16 H=16 D=64/128 L=8k, 1 MI355X"
 PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 COPY_BYTES = 256 * 2**20  # calibration copy: bytes read = bytes written
 
 
@@ -100,6 +102,20 @@ def make_config(cfg: int):
         return dict(q=q, k=k, v=v, kw=dict(causal=True, window_size=(2048, 0), softcap=30.0, alibi_slopes=slopes),
                     dtype="bf16", D=D, formula=4 * B * H * L * L * D // 2, algo=4 * pairs * D, varlen=None,
                     workload="cfg5: bf16 B=1 L=32768 H=16 D=128 causal window=(2048,0) softcap=30 ALiBi, seed 4")
+    if cfg in (6, 7):
+        # not BASELINE configs: the short-L, HBM-bound shapes the metric asks
+        # HBM GB/s for (6: short sequences, 7: one query row per sequence)
+        g = torch.Generator().manual_seed(cfg)
+        B, H, D = 64, 16, 64
+        Lq, Lk = (256, 256) if cfg == 6 else (1, 4096)
+        q = torch.randn(B, Lq, H, D, generator=g).to(dev, torch.bfloat16)
+        k = torch.randn(B, Lk, H, D, generator=g).to(dev, torch.bfloat16)
+        v = torch.randn(B, Lk, H, D, generator=g).to(dev, torch.bfloat16)
+        pairs = B * H * Lq * Lk
+        return dict(q=q, k=k, v=v, kw=dict(causal=False), dtype="bf16", D=D, formula=4 * pairs * D,
+                    algo=4 * pairs * D, varlen=None, hbm_bytes=2 * (2 * B * Lq * H * D + 2 * B * Lk * H * D),
+                    workload=f"cfg{cfg} (HBM-bound, not a BASELINE config): bf16 B={B} Lq={Lq} Lk={Lk} "
+                             f"H={H} D={D} non-causal, seed {cfg}")
     raise SystemExit(f"unknown config {cfg}")
 
 
@@ -171,7 +187,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7],
+                    help="BASELINE config 2-5 (default 2, the headline); 6 and 7 are HBM-bound short-L "
+                         "shapes (roofline in GB/s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, run one plain 256 MiB device copy (rocprofv3 PMC calibration of "
@@ -245,6 +263,12 @@ def main():
                      "kernel_ms": round(kernel_ms, 4),
                      "note": "algorithmic FLOPs (4*D per valid (query,key) pair) / mean launch time"},
     }
+    if "hbm_bytes" in c:
+        gbs = c["hbm_bytes"] / (kernel_ms / 1e3) / 1e9
+        line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kname,
+                            "kernel_ms": round(kernel_ms, 4), "algorithmic_bytes": c["hbm_bytes"],
+                            "note": "algorithmic bytes (Q + K + V + O, each once) / mean launch time"}
     if args.copy_calibration:
         x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
         y = torch.empty_like(x)

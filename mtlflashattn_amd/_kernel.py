@@ -318,4 +318,8 @@ def launch_info(q, k, v, causal=False, softcap=0.0, alibi=False, window_left=-1,
     p.window_left, p.window_right, p.causal = window_left, window_right, int(causal)
     p.alibi_slopes = 256 if alibi else None
     p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
+    hint = _TILE_HINT
+    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and p.head_dim > 64):
+        hint = _hip.MFA_TILE_AUTO
+    p.tile_hint = hint
     return _hip.launch_info(p)

@@ -1576,8 +1576,13 @@ int make_plan(const mfa_fwd_params* p, Plan* plan) {
         return set_err(MFA_ERR_INVALID, "mfa_fwd: unknown tile_hint %d", p->tile_hint);
     if (p->tile_hint == MFA_TILE_PINGPONG && (din == MFA_DTYPE_F32 || dp > 64))
         return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles need bf16/fp16 and head_dim <= 64");
+    // Auto: 512-row ping-pong tiles when they fill the chip (one workgroup
+    // per CU) and leave at most 25% more rows empty than 256-row tiles do
+    // (short or single-row queries run faster on the 4-wavefront kernel).
+    const int64_t rows512 = (int64_t)((p->seqlen_q + 511) / 512) * 512;
+    const int64_t rows256 = (int64_t)((p->seqlen_q + 255) / 256) * 256;
     const bool fills_chip = p->tile_hint == MFA_TILE_AUTO
-                                ? (int64_t)p->batch * p->heads_q * ((p->seqlen_q + 511) / 512) >= 256
+                                ? (int64_t)p->batch * p->heads_q * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256
                                 : p->tile_hint == MFA_TILE_PINGPONG;
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp) : select32<false>(dp);

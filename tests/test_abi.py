@@ -128,6 +128,14 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     small = torch.empty(1, 2048, 16, 64, dtype=torch.bfloat16)
     info = _kernel.launch_info(small, small, small)
     assert info.block_x == 256 and info.kernel_name.startswith(b"mfa_fwd16<bf16,d64")
+    # many short or single-row sequences: half-empty 512-row tiles lose to the
+    # 256-row kernel even on a full grid (HBM-bound shapes)
+    for lq, lk in ((256, 256), (1, 4096), (768, 768)):
+        qs = torch.empty(64, lq, 16, 64, dtype=torch.bfloat16)
+        ks = torch.empty(64, lk, 16, 64, dtype=torch.bfloat16)
+        assert _kernel.launch_info(qs, ks, ks).block_x == 256, (lq, lk)
+    long = torch.empty(8, 1280, 16, 64, dtype=torch.bfloat16)
+    assert _kernel.launch_info(long, long, long).block_x == 512
     # the tile hint overrides the automatic choice
     p = good_params(L=2048, H=16)
     p.tile_hint = _hip.MFA_TILE_PINGPONG
