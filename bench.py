@@ -14,8 +14,8 @@ Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
   cpu_baseline : the reference's chunked-fp32 torch path (oracle/chunked.py)
                  timed on this host's cores on a bounded sample of the same
                  workload (a subset of heads).
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7]
-(6 and 7: HBM-bound short-L shapes, roofline in GB/s against 8 TB/s)
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7|8]
+(6-8: HBM-bound short-L shapes, roofline in GB/s against 8 TB/s; 8 runs split-KV)
 """
 from __future__ import annotations
 
@@ -102,12 +102,13 @@ def make_config(cfg: int):
         return dict(q=q, k=k, v=v, kw=dict(causal=True, window_size=(2048, 0), softcap=30.0, alibi_slopes=slopes),
                     dtype="bf16", D=D, formula=4 * B * H * L * L * D // 2, algo=4 * pairs * D, varlen=None,
                     workload="cfg5: bf16 B=1 L=32768 H=16 D=128 causal window=(2048,0) softcap=30 ALiBi, seed 4")
-    if cfg in (6, 7):
+    if cfg in (6, 7, 8):
         # not BASELINE configs: the short-L, HBM-bound shapes the metric asks
-        # HBM GB/s for (6: short sequences, 7: one query row per sequence)
+        # HBM GB/s for (6: short sequences, 7: one query row per sequence,
+        # 8: one long decode row per head, run split-KV)
         g = torch.Generator().manual_seed(cfg)
-        B, H, D = 64, 16, 64
-        Lq, Lk = (256, 256) if cfg == 6 else (1, 4096)
+        B, H, D = (64, 16, 64) if cfg != 8 else (1, 16, 128)
+        Lq, Lk = {6: (256, 256), 7: (1, 4096), 8: (1, 131072)}[cfg]
         q = torch.randn(B, Lq, H, D, generator=g).to(dev, torch.bfloat16)
         k = torch.randn(B, Lk, H, D, generator=g).to(dev, torch.bfloat16)
         v = torch.randn(B, Lk, H, D, generator=g).to(dev, torch.bfloat16)
@@ -187,9 +188,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7],
-                    help="BASELINE config 2-5 (default 2, the headline); 6 and 7 are HBM-bound short-L "
-                         "shapes (roofline in GB/s)")
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8],
+                    help="BASELINE config 2-5 (default 2, the headline); 6-8 are HBM-bound short-L "
+                         "shapes (roofline in GB/s; 8 runs split-KV)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, run one plain 256 MiB device copy (rocprofv3 PMC calibration of "
@@ -242,6 +243,9 @@ def main():
                                    window_left=c["kw"].get("window_size", (-1, -1))[0],
                                    window_right=c["kw"].get("window_size", (-1, -1))[1])
         kname = info.kernel_name.decode()
+        chunk = _kernel.split_chunk(c["q"], c["k"])
+        if chunk:
+            kname += f" split-KV {chunk} keys + mfa_combine"
     traffic = measured_traffic(args.config)
     line = {
         "metric": METRIC,

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MFA_ABI_VERSION 1
+#define MFA_ABI_VERSION 2
 
 /* element types (dtype_in / dtype_out) */
 #define MFA_DTYPE_F16 0
@@ -154,6 +154,32 @@ int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info);
 /* sizeof(mfa_fwd_params) as compiled into the library, so FFI bindings can
  * check their struct mirror.  No counterpart in the reference. */
 int mfa_params_size(void);
+
+/* Split-KV forward for decode-like shapes (few query rows, long key ranges):
+ * the key range of every sequence is cut into chunks of `split_keys` keys,
+ * workgroups compute the chunks in parallel into a caller-provided
+ * workspace, and a second kernel merges them (log-sum-exp weighting).  No
+ * counterpart in the reference, whose Metal kernels run one threadgroup per
+ * query tile over all keys; these three calls are the build's addition for
+ * HBM-bound shapes.  bf16/fp16 only; results meet the same bars as mfa_fwd.
+ *
+ * mfa_fwd_split_keys: the library's choice for `params`, 0 = use mfa_fwd.
+ * It is 2048 when seqlen_q (the longest query for varlen) is at most 256 and
+ * seqlen_k exceeds 2048, else 0 (fp32 and forced ping-pong tiles: 0); a
+ * dense call with batch > 1 and batch * heads_q >= 512 gets 0 too (the
+ * single pass already fills the chip).  For varlen and batch = 1 calls the
+ * choice depends on the lengths only, so a sequence is chunked alike alone or
+ * inside a varlen batch (bit-identical rows either way).
+ * mfa_fwd_workspace_bytes: device bytes mfa_fwd_splitkv needs for this call
+ * and chunk size (0 for split_keys 0 or an empty problem; < 0 on error).
+ * mfa_fwd_splitkv: enqueue both kernels on `stream`; `workspace` is a
+ * 256-byte aligned device buffer of at least that many bytes, owned by the
+ * caller and reused only after the call's kernels ran (stream order).
+ * split_keys must be 0 (same as mfa_fwd) or a positive multiple of 64. */
+int32_t mfa_fwd_split_keys(const mfa_fwd_params* params);
+int64_t mfa_fwd_workspace_bytes(const mfa_fwd_params* params, int32_t split_keys);
+int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime first)
 
 from ._build import LIB_PATH
 
-MFA_ABI_VERSION = 1
+MFA_ABI_VERSION = 2
 MFA_DTYPE_F16 = 0
 MFA_DTYPE_BF16 = 1
 MFA_DTYPE_F32 = 2
@@ -115,6 +115,12 @@ def load():
         lib.mfa_fwd.argtypes = [ctypes.POINTER(MfaFwdParams), _c_ptr]
         lib.mfa_fwd_launch_info.restype = ctypes.c_int
         lib.mfa_fwd_launch_info.argtypes = [ctypes.POINTER(MfaFwdParams), ctypes.POINTER(MfaLaunchInfo)]
+        lib.mfa_fwd_split_keys.restype = _c_i32
+        lib.mfa_fwd_split_keys.argtypes = [ctypes.POINTER(MfaFwdParams)]
+        lib.mfa_fwd_workspace_bytes.restype = ctypes.c_int64
+        lib.mfa_fwd_workspace_bytes.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32]
+        lib.mfa_fwd_splitkv.restype = ctypes.c_int
+        lib.mfa_fwd_splitkv.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32, _c_ptr, ctypes.c_int64, _c_ptr]
         if lib.mfa_abi_version() != MFA_ABI_VERSION:
             raise HipLibraryError(
                 f"mtlflashattn_amd: {path} has ABI {lib.mfa_abi_version()}, expected {MFA_ABI_VERSION}; rebuild it"
@@ -146,6 +152,27 @@ def fwd(params: MfaFwdParams, stream: int) -> None:
     rc = lib.mfa_fwd(ctypes.byref(params), _c_ptr(stream))
     if rc != MFA_OK:
         raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_fwd failed ({rc})")
+
+
+def split_keys(params: MfaFwdParams) -> int:
+    """The library's split-KV chunk size for this call (0: no split)."""
+    return int(load().mfa_fwd_split_keys(ctypes.byref(params)))
+
+
+def workspace_bytes(params: MfaFwdParams, chunk: int) -> int:
+    lib = load()
+    n = lib.mfa_fwd_workspace_bytes(ctypes.byref(params), int(chunk))
+    if n < 0:
+        raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_fwd_workspace_bytes failed ({n})")
+    return int(n)
+
+
+def fwd_splitkv(params: MfaFwdParams, chunk: int, workspace: int, workspace_bytes_: int, stream: int) -> None:
+    lib = load()
+    rc = lib.mfa_fwd_splitkv(ctypes.byref(params), int(chunk), _c_ptr(workspace), int(workspace_bytes_),
+                             _c_ptr(stream))
+    if rc != MFA_OK:
+        raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_fwd_splitkv failed ({rc})")
 
 
 def launch_info(params: MfaFwdParams) -> MfaLaunchInfo:

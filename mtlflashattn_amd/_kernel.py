@@ -47,6 +47,10 @@ _warned_modes = set()
 # tests set it to run every case through each kernel.  A preference the launch
 # cannot take (fp32, ping-pong with a head dim above 64) falls back to 0.
 _TILE_HINT = 0
+# Split-KV chunk in keys for bf16/fp16 calls: None = the library's choice
+# (mfa_fwd_split_keys), 0 = never split, a multiple of 64 = that chunk
+# (tests and tuning).
+_SPLIT_KEYS = None
 
 
 def _kernel_mode() -> str:
@@ -212,8 +216,19 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and Dp > 64):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
+    chunk = 0
+    if q.dtype != torch.float32 and hint != _hip.MFA_TILE_PINGPONG:
+        chunk = _hip.split_keys(p) if _SPLIT_KEYS is None else _SPLIT_KEYS
     with torch.cuda.device(q.device):
-        _hip.fwd(p, torch.cuda.current_stream(q.device).cuda_stream)
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        if chunk:
+            # split-KV: partials in a workspace from torch's stream-ordered
+            # caching allocator (reused only after these kernels ran)
+            nbytes = _hip.workspace_bytes(p, chunk)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+            _hip.fwd_splitkv(p, chunk, ws.data_ptr(), nbytes, stream)
+        else:
+            _hip.fwd(p, stream)
     if dst is not out:
         out.copy_(dst[..., :D])
     return out
@@ -300,6 +315,18 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
     return _run(q[None], k[None], v[None], out[None], scale=scale, causal=causal, softcap=softcap,
                 window_left=window_left, window_right=window_right, alibi=alibi, alibi_bstride=bstride,
                 cu_q=cu_q, cu_k=cu_k, seqlen_q=max_q, seqlen_k=max_k)[0]
+
+
+def split_chunk(q, k):
+    """Split-KV chunk (keys) the library picks for heads-third q/k (0: single pass)."""
+    if q.dtype == torch.float32:
+        return 0
+    p = _hip.MfaFwdParams()
+    p.batch, p.heads_q, p.heads_kv = q.shape[0], q.shape[2], k.shape[2]
+    p.seqlen_q, p.seqlen_k = q.shape[1], k.shape[1]
+    p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
+    p.tile_hint = _TILE_HINT
+    return _hip.split_keys(p) if _SPLIT_KEYS is None else _SPLIT_KEYS
 
 
 def launch_info(q, k, v, causal=False, softcap=0.0, alibi=False, window_left=-1, window_right=-1):

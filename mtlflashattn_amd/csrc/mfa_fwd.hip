@@ -131,6 +131,15 @@ struct KArgs {
     int32_t U;        // (sequence, head) units = B * Hq
     int32_t upx;      // units per XCD (grouped schedule)
     int32_t grouped;  // 1: XCD-grouped by K/V head, 0: linear
+    // split-KV: the key range of a sequence is cut into chunks of split_keys
+    // keys (a multiple of the key block); workgroup (tile, split) writes the
+    // chunk's normalised O and log2-sum-exp to the workspace, the combine
+    // kernel merges them.  nsplit = chunks of the longest sequence (<= 1: off).
+    int32_t nsplit;
+    int32_t split_keys;
+    int32_t ws_ld;    // floats per workspace O row (padded head dim)
+    float* ws_o;      // [nsplit][U][Lq][ws_ld]
+    float* ws_lse;    // [nsplit][U][Lq]
 };
 
 // ----------------------------------------------------------------------------
@@ -505,6 +514,97 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
     }
 }
 
+// Split-KV partial of one chunk: O normalised by the chunk's own row sum and
+// the chunk's log2-sum-exp lse = mu + log2(l) (probabilities were
+// exp2(x - mu)); a row with no valid key in the chunk gets lse = -inf, O = 0.
+template <int QB, int DB>
+__device__ __forceinline__ void store_partial(const KArgs& a, int Lq, int unit, int split, f32x16_t (&o)[QB][DB],
+                                              const RowState (&rs)[QB], float c, int qrow0, int lane) {
+    const int l32 = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const float l = sum_halves(rs[qb].l);
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const int qrow = qrow0 + 32 * qb + l32;
+        if (qrow >= Lq) continue;
+        const int64_t row = ((int64_t)split * a.U + unit) * a.Lq + qrow;
+        if (half == 0) {
+            const float mu = rs[qb].m == -INFINITY ? 0.f : rs[qb].m * c;
+            a.ws_lse[row] = l > 0.f ? mu + __builtin_amdgcn_logf(l) : -INFINITY;
+        }
+        float* dst = a.ws_o + row * a.ws_ld;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * db + 8 * g + 4 * half;
+                if (d >= a.D) continue;
+                *reinterpret_cast<float4*>(dst + d) =
+                    make_float4(o[qb][db][4 * g] * inv, o[qb][db][4 * g + 1] * inv, o[qb][db][4 * g + 2] * inv,
+                                o[qb][db][4 * g + 3] * inv);
+            }
+    }
+}
+
+// Merge of the split-KV partials, one wavefront per query row.  A sequence
+// uses ceil(Lk / split_keys) chunks (one when it has no key); O =
+// sum_s w_s O_s / sum_s w_s with w_s = 2^(lse_s - M), M = max_s lse_s, and 0
+// when no chunk has a valid key (a fully masked row, _kernel.py:85-86).  The
+// lanes read the chunks' lse in parallel (max and weight sum reduced across
+// the wavefront, weights kept in LDS), then each lane sums its two head-dim
+// elements over the chunks in chunk order with independent loads.  With one
+// chunk the weight is exactly 1 and O is the chunk's O unchanged.
+constexpr int kMaxSplits = 1024;
+template <bool IS_BF16>
+__global__ void __launch_bounds__(64) mfa_combine_kernel(KArgs a) {
+    __shared__ float wsh[kMaxSplits];
+    const int lane = threadIdx.x;
+    const int64_t r = blockIdx.x;  // row (unit, query row)
+    const int unit = (int)(r / a.Lq), qrow = (int)(r % a.Lq);
+    const int b = unit / a.Hq, hq = unit - b * a.Hq;
+    const SeqView sv = seq_view<2>(a, b, hq);
+    if (qrow >= sv.Lq) return;
+    const int ns = min(a.nsplit, max(1, (sv.Lk + a.split_keys - 1) / a.split_keys));
+    const int64_t stride = (int64_t)a.U * a.Lq;
+    float m = -INFINITY;
+    for (int sp = lane; sp < ns; sp += 64) m = fmaxf(m, a.ws_lse[sp * stride + r]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float wsum = 0.f;
+    for (int sp = lane; sp < ns; sp += 64) {
+        const float lse = a.ws_lse[sp * stride + r];
+        const float w = m == -INFINITY || lse == -INFINITY ? 0.f : fast_exp2(lse - m);
+        wsh[sp] = w;
+        wsum += w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wsum += __shfl_xor(wsum, o);
+    __syncthreads();
+    const int d = 2 * lane;
+    if (d >= a.D) return;
+    float acc0 = 0.f, acc1 = 0.f;
+    if (m != -INFINITY) {
+        const float* src = a.ws_o + r * a.ws_ld + d;
+#pragma unroll 8
+        for (int sp = 0; sp < ns; ++sp) {
+            const float2 x = *reinterpret_cast<const float2*>(src + sp * stride * a.ws_ld);
+            acc0 = fmaf(wsh[sp], x.x, acc0);
+            acc1 = fmaf(wsh[sp], x.y, acc1);
+        }
+        acc0 /= wsum;
+        acc1 /= wsum;
+    }
+    if (a.out_f32) {
+        *reinterpret_cast<float2*>(reinterpret_cast<float*>(sv.o) + (int64_t)qrow * a.os + d) = make_float2(acc0, acc1);
+    } else if constexpr (IS_BF16) {
+        const bf16x2_t w = {(__bf16)acc0, (__bf16)acc1};
+        *reinterpret_cast<bf16x2_t*>(reinterpret_cast<__bf16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+    } else {
+        const f16x2_t w = {(_Float16)acc0, (_Float16)acc1};
+        *reinterpret_cast<f16x2_t*>(reinterpret_cast<_Float16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+    }
+}
+
 // ----------------------------------------------------------------------------
 // 16-bit (bf16 / fp16) kernel.
 //   DP  : head dim padded to a multiple of 32 (32, 64, 96, 128)
@@ -538,9 +638,16 @@ mfa_fwd16_kernel(KArgs a) {
 
     int b, hq, tile;
     if (!decode_tile(a, blockIdx.x, b, hq, tile)) return;
+    int split = 0;
+    if (a.nsplit > 1) {
+        split = tile % a.nsplit;
+        tile /= a.nsplit;
+    }
     const SeqView sv = seq_view<2>(a, b, hq);
     const int q0 = tile * BM;
     if (q0 >= sv.Lq) return;
+    // split-KV: this sequence's chunks (one when it has no key)
+    if (a.nsplit > 1 && split >= max(1, (sv.Lk + a.split_keys - 1) / a.split_keys)) return;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
@@ -589,8 +696,17 @@ mfa_fwd16_kernel(KArgs a) {
     const int qlast = min(q0 + BM, Lq) - 1;
     const int klo = key_lo(a, q0 + dq);
     const int khi = key_hi(a, qlast + dq, Lk);
-    const int jbeg = (klo / BN) * BN;
-    const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
+    int jbeg = (klo / BN) * BN;
+    int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
+    int kend = Lk;  // loads read zero from key kend on
+    if (a.nsplit > 1) {
+        // split-KV: the blocks of chunk `split` (chunks are whole blocks)
+        const int c0 = split * a.split_keys, c1 = c0 + a.split_keys;
+        const int j0 = max(jbeg, c0), j1 = min(jbeg + nblk * BN, c1);
+        nblk = j1 > j0 ? (j1 - j0) / BN : 0;
+        jbeg = j0;
+        kend = min(Lk, c1);
+    }
     const int wlast = min(wq0 + QB * 32, Lq) - 1;  // < wq0 when the wave has no rows
     const bool wave_live = wlast >= wq0;
     const int w_lo_first = key_lo(a, wq0 + dq), w_lo_last = key_lo(a, wlast + dq);
@@ -618,7 +734,7 @@ mfa_fwd16_kernel(KArgs a) {
         // rows <= 0 (a block past the sequence, loaded branch-free by the
         // pipelined path) gives an empty resource: every lane reads zero
         // (computed without branches, so the pipelined block stays one basic block)
-        const int rows = Lk - j;
+        const int rows = kend - j;
         const int rm1 = min(max(rows, 1), BN) - 1;
         const int live = -(int)(rows > 0);
         const int kbytes = (int)(((int64_t)rm1 * a.ks + D) * 2) & live;
@@ -870,7 +986,10 @@ mfa_fwd16_kernel(KArgs a) {
         __syncthreads();
     }
 
-    store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
+    if (a.nsplit > 1)
+        store_partial<QB, DB>(a, Lq, b * a.Hq + hq, split, o, rs, c, wq0, lane);
+    else
+        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -1513,11 +1632,13 @@ struct Plan {
     KArgs args;
     int grid;
     bool empty;
+    kernel_fn combine = nullptr;  // split-KV merge kernel
+    int64_t ws_bytes = 0;         // split-KV workspace
 };
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int make_plan(const mfa_fwd_params* p, Plan* plan) {
+int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     if (!p) return set_err(MFA_ERR_INVALID, "mfa_fwd: params is NULL");
     const int din = p->dtype_in, dout = p->dtype_out;
     if (din != MFA_DTYPE_F16 && din != MFA_DTYPE_BF16 && din != MFA_DTYPE_F32)
@@ -1581,9 +1702,19 @@ int make_plan(const mfa_fwd_params* p, Plan* plan) {
     // (short or single-row queries run faster on the 4-wavefront kernel).
     const int64_t rows512 = (int64_t)((p->seqlen_q + 511) / 512) * 512;
     const int64_t rows256 = (int64_t)((p->seqlen_q + 255) / 256) * 256;
-    const bool fills_chip = p->tile_hint == MFA_TILE_AUTO
-                                ? (int64_t)p->batch * p->heads_q * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256
-                                : p->tile_hint == MFA_TILE_PINGPONG;
+    bool fills_chip = p->tile_hint == MFA_TILE_AUTO
+                          ? (int64_t)p->batch * p->heads_q * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256
+                          : p->tile_hint == MFA_TILE_PINGPONG;
+    if (split_keys != 0) {
+        // split-KV runs on the 4-wavefront kernel (bf16/fp16)
+        if (split_keys < 0 || split_keys % 64 != 0)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: split_keys %d must be a positive multiple of 64",
+                           split_keys);
+        if (din == MFA_DTYPE_F32) return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd_splitkv: fp32 has no split-KV path");
+        if (p->tile_hint == MFA_TILE_PINGPONG)
+            return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd_splitkv: split-KV uses the 256-row tiles");
+        fills_chip = false;
+    }
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp) : select32<false>(dp);
     else if (din == MFA_DTYPE_BF16)
@@ -1632,8 +1763,43 @@ int make_plan(const mfa_fwd_params* p, Plan* plan) {
         plan->grid = a.U * a.T;
     }
     if ((int64_t)a.U * a.T > 0x7fffffffLL / 2) return set_err(MFA_ERR_INVALID, "mfa_fwd: problem too large");
+    a.nsplit = 1;
+    if (split_keys != 0) {
+        const int ns = (p->seqlen_k + split_keys - 1) / split_keys;
+        if (ns > kMaxSplits)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: %d chunks of %d keys exceed %d; use larger chunks", ns,
+                           split_keys, kMaxSplits);
+        a.nsplit = ns > 1 ? ns : 1;
+        a.split_keys = split_keys;
+        a.ws_ld = dp;
+        if ((int64_t)a.U * a.T * a.nsplit > 0x7fffffffLL / 2)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: too many splits");
+        a.T *= a.nsplit;
+        plan->grid *= a.nsplit;
+        const int64_t rows = (int64_t)a.nsplit * a.U * p->seqlen_q;
+        plan->ws_bytes = rows * dp * 4 + ((rows * 4 + 255) / 256) * 256;
+        plan->combine = din == MFA_DTYPE_BF16 ? (kernel_fn)mfa_combine_kernel<true> : (kernel_fn)mfa_combine_kernel<false>;
+    }
     if (plan->grid == 0) plan->empty = true;
     return MFA_OK;
+}
+
+// Split-KV is chosen for decode-like calls: at most 256 query rows per
+// sequence (one or two query tiles) and more keys than one chunk.  The chunk is a constant (2048 keys: on MI355X
+// the best single size over B=1..64, Hq=16..32, Lk=8K..128K decode shapes).
+// For varlen and B=1 calls the choice depends on the lengths only, so a
+// sequence gets the same chunks alone (dense B=1) or inside a varlen batch
+// and its rows are bit-identical either way.  A dense batch whose
+// (sequence, head) units already fill the chip (>= 512 workgroups) runs the
+// single pass: there the split's merge and extra workgroups cost ~8%.
+constexpr int kSplitMaxLq = 256;
+constexpr int kSplitKeys = 2048;
+constexpr int64_t kSplitMaxUnits = 512;
+int auto_split_keys(const mfa_fwd_params* p) {
+    if (!p || p->dtype_in == MFA_DTYPE_F32 || p->tile_hint == MFA_TILE_PINGPONG) return 0;
+    if (p->seqlen_q > kSplitMaxLq || p->seqlen_k <= kSplitKeys) return 0;
+    if (!p->cu_seqlens_q && p->batch > 1 && (int64_t)p->batch * p->heads_q >= kSplitMaxUnits) return 0;
+    return kSplitKeys;
 }
 
 }  // namespace
@@ -1664,6 +1830,44 @@ int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info) {
     info->lds_bytes = plan.cfg.lds;
     snprintf(info->kernel_name, sizeof(info->kernel_name), "%s%s", plan.cfg.name,
              (params->softcap > 0.f || params->alibi_slopes) ? "+bias" : "");
+    return MFA_OK;
+}
+
+int32_t mfa_fwd_split_keys(const mfa_fwd_params* params) { return auto_split_keys(params); }
+
+int64_t mfa_fwd_workspace_bytes(const mfa_fwd_params* params, int32_t split_keys) {
+    g_err[0] = 0;
+    if (split_keys == 0) return 0;
+    Plan plan;
+    const int rc = make_plan(params, &plan, split_keys);
+    if (rc != MFA_OK) return rc;
+    return plan.empty ? 0 : plan.ws_bytes;
+}
+
+int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
+    g_err[0] = 0;
+    if (split_keys == 0) return mfa_fwd(params, stream);
+    Plan plan;
+    const int rc = make_plan(params, &plan, split_keys);
+    if (rc != MFA_OK) return rc;
+    if (plan.empty) return MFA_OK;
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: workspace must be a 256-byte aligned device pointer");
+    if (workspace_bytes < plan.ws_bytes)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: workspace of %lld bytes, %lld needed",
+                       (long long)workspace_bytes, (long long)plan.ws_bytes);
+    KArgs& a = plan.args;
+    const int64_t rows = (int64_t)a.nsplit * a.U * params->seqlen_q;
+    a.ws_o = static_cast<float*>(workspace);
+    a.ws_lse = a.ws_o + rows * a.ws_ld;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // one chunk (every key range fits): the kernel stores O itself
+    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, st, a);
+    if (a.nsplit > 1)
+        hipLaunchKernelGGL(plan.combine, dim3((unsigned)((int64_t)a.U * params->seqlen_q)), dim3(64), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd_splitkv: launch failed: %s", hipGetErrorString(e));
     return MFA_OK;
 }
 

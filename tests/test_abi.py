@@ -32,7 +32,8 @@ def declared_functions():
 
 def test_header_declares_the_entry_points():
     assert set(declared_functions()) >= {"mfa_abi_version", "mfa_last_error", "mfa_supported", "mfa_fwd",
-                                         "mfa_fwd_launch_info", "mfa_params_size"}
+                                         "mfa_fwd_launch_info", "mfa_params_size", "mfa_fwd_split_keys",
+                                         "mfa_fwd_workspace_bytes", "mfa_fwd_splitkv"}
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -160,3 +161,76 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_hip, "_lib", None)
     with pytest.raises(_hip.HipLibraryError, match="not found"):
         _hip.load()
+
+
+def test_split_kv_choice(lib):
+    # decode-like: few query rows, more keys than one 2048-key chunk
+    for B in (1, 8):
+        p = good_params(B=B, L=4096, H=16)
+        p.seqlen_q = 1
+        assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 2048
+        p.seqlen_q = 256
+        assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 2048
+        p.seqlen_q = 257
+        assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 0
+    p = good_params(L=2048)
+    p.seqlen_q = 1
+    assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 0
+    p.seqlen_k = 2049
+    assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 2048
+    # a dense batch that fills the chip on its own keeps the single pass; a
+    # varlen batch (or B=1) is chunked by its lengths alone
+    p = good_params(B=64, L=4096, H=16)
+    p.seqlen_q = 1
+    assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 0
+    p.cu_seqlens_q = p.cu_seqlens_k = 256
+    assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 2048
+    p = good_params(B=1, L=4096, H=1024)
+    p.seqlen_q = 1
+    assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 2048
+    p = good_params(L=8192, dtype=_hip.MFA_DTYPE_F32)
+    p.seqlen_q = 1
+    assert lib.mfa_fwd_split_keys(ctypes.byref(p)) == 0
+    assert lib.mfa_fwd_split_keys(None) == 0
+
+
+def test_split_kv_workspace_size(lib):
+    p = good_params(B=2, L=3000, H=8, Hkv=2, D=64)
+    p.seqlen_q = 3
+    # ceil(3000 / 1024) = 3 chunks x (2*8 units) x 3 rows: O rows of 64 floats + lse (256-byte aligned)
+    rows = 3 * 16 * 3
+    assert lib.mfa_fwd_workspace_bytes(ctypes.byref(p), 1024) == rows * 64 * 4 + -(-rows * 4 // 256) * 256
+    assert lib.mfa_fwd_workspace_bytes(ctypes.byref(p), 0) == 0
+    p.head_dim = 40  # padded to 64-float rows
+    assert lib.mfa_fwd_workspace_bytes(ctypes.byref(p), 1024) == rows * 64 * 4 + -(-rows * 4 // 256) * 256
+
+
+@pytest.mark.parametrize("chunk,mutate,code,msg", [
+    (100, None, _hip.MFA_ERR_INVALID, "multiple of 64"),
+    (-64, None, _hip.MFA_ERR_INVALID, "multiple of 64"),
+    (1024, lambda p: setattr(p, "dtype_in", _hip.MFA_DTYPE_F32) or setattr(p, "dtype_out", _hip.MFA_DTYPE_F32),
+     _hip.MFA_ERR_UNSUPPORTED, "fp32"),
+    (1024, lambda p: setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), _hip.MFA_ERR_UNSUPPORTED, "256-row"),
+    (64, lambda p: setattr(p, "seqlen_k", 64 * 1025), _hip.MFA_ERR_INVALID, "exceed"),
+])
+def test_split_kv_invalid_requests(lib, chunk, mutate, code, msg):
+    p = good_params(L=4096)
+    p.seqlen_q = 1
+    if mutate:
+        mutate(p)
+    assert lib.mfa_fwd_workspace_bytes(ctypes.byref(p), chunk) == code
+    assert lib.mfa_fwd_splitkv(ctypes.byref(p), chunk, ctypes.c_void_p(1 << 20), 1 << 30, None) == code
+    assert msg in lib.mfa_last_error().decode()
+
+
+def test_split_kv_rejects_a_small_or_misaligned_workspace(lib):
+    p = good_params(L=4096)
+    p.seqlen_q = 1
+    need = lib.mfa_fwd_workspace_bytes(ctypes.byref(p), 1024)
+    assert need > 0
+    assert lib.mfa_fwd_splitkv(ctypes.byref(p), 1024, ctypes.c_void_p(1 << 20), need - 1, None) == _hip.MFA_ERR_INVALID
+    assert b"needed" in lib.mfa_last_error()
+    assert lib.mfa_fwd_splitkv(ctypes.byref(p), 1024, ctypes.c_void_p((1 << 20) + 16), need, None) == \
+        _hip.MFA_ERR_INVALID
+    assert b"aligned" in lib.mfa_last_error()
+    assert lib.mfa_fwd_splitkv(ctypes.byref(p), 1024, None, need, None) == _hip.MFA_ERR_INVALID
