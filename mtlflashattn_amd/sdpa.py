@@ -8,18 +8,29 @@ fires, and otherwise -- or when the kernel raises -- calls the original op.
 It never crashes the caller.  Kill switch: MTLFLASHATTN_SDPA=off.
 
 Gates (any one fires; thresholds from the arguments or the
-MTLFLASHATTN_SDPA_* environment variables, defaults as in the reference):
+MTLFLASHATTN_SDPA_* environment variables):
   1. "correctness-large-seq": max(Lq, Lk) >= min_seq (default 4096).  On MPS
      this shielded a stock-SDPA accuracy bug; on ROCm it keeps long sequences
-     on the O(L*D)-memory kernel.
-  2. "fast-tier": max(Lq, Lk) >= fast_min_seq (default 1024) and the inputs
-     take the fast MFMA path (fp16/bf16, head_dim a multiple of 8).
+     on the O(L*D)-memory kernel (faster than stock there for every dtype).
+  2. "fast-tier": max(Lq, Lk) >= fast_min_seq (default 512) and the inputs
+     take an MFMA path that beats stock ROCm SDPA: fp16/bf16 or fp32 with
+     head_dim a multiple of 8.
   3. "oom-rescue": the Lq x Lk score matrix would take >= min_score_gb
      (default 12 GB) as fp16.
+The fast-tier floor and tiers are re-derived for ROCm (the reference's 1024
+floor and its tier set were measured against stock MPS SDPA): on MI355X with
+torch 2.10 the HIP path matches or beats stock SDPA from 512 tokens in
+fp16/bf16 (0.94-2.3x at 512, 1.0-2.0x beyond) and from 256 in fp32, and loses
+below 512 in fp16/bf16 (host launch cost dominates there).  Re-measure on
+another machine with `python -m mtlflashattn_amd.sdpa_sweep`.
 
-Not carried over: the reference's uneven-value-head-dim shield
-(metal_flash_attn/sdpa.py:76-130, :145-149), a guard against a stock-SDPA
-bug on MPS; on ROCm such calls go to the original op.
+Value head dim != query/key head dim (the reference's uneven-V shield,
+metal_flash_attn/sdpa.py:76-130, :145-149, an exact torch path): gated like
+the even case and computed by the HIP kernel, exactly, on zero-padded head
+dims (zero query/key columns add nothing to a score; padded value columns are
+dropped), one launch per 128 value columns.  Calls the kernel cannot express
+(attention masks, top-left causal with Lq != Lk) go to the original op, which
+handles uneven V on ROCm.
 """
 from __future__ import annotations
 
@@ -33,8 +44,8 @@ from ._kernel import MAX_HEAD_DIM, flash_attn_forward
 
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
-# tiers of the single HIP path that beat stock SDPA (see _select_tier)
-_FAST_TIERS = frozenset({"hip"})
+# tiers of the single HIP path that beat stock ROCm SDPA (see _select_tier)
+_FAST_TIERS = frozenset({"hip", "hip-fp32"})
 
 _orig = None
 _min_score_bytes = None
@@ -86,7 +97,7 @@ def _eligibility(q, k, v, attn_mask, dropout_p, is_causal):
     if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         return False, f"dtype({q.dtype})"
     D = q.shape[-1]
-    if D > MAX_HEAD_DIM or k.shape[-1] != D or v.shape[-1] != D:
+    if D > MAX_HEAD_DIM or k.shape[-1] != D or v.shape[-1] < 1:
         return False, f"head_dim({D})"
     Hq, Hkv = q.shape[1], k.shape[1]
     if Hkv == 0 or Hq % Hkv != 0:
@@ -100,11 +111,28 @@ def _eligibility(q, k, v, attn_mask, dropout_p, is_causal):
     return _gate(q.shape[0], Hq, Lq, Lk, _select_tier(q, k, v))
 
 
+def _uneven_v(q, k, v, scale, causal):
+    """[B,H,L,D] attention with value head dim Dv != D on the HIP kernel: the
+    narrower of (q/k, v) is zero-padded to the wider, Dv in blocks of at most
+    MAX_HEAD_DIM columns (one launch each); exact (zero columns add nothing)."""
+    D, Dv = q.shape[-1], v.shape[-1]
+    outs = []
+    for c0 in range(0, Dv, MAX_HEAD_DIM):
+        vc = v[..., c0:c0 + MAX_HEAD_DIM]
+        w = max(D, vc.shape[-1])
+        qp, kp = (F.pad(t, (0, w - D)) if w > D else t for t in (q, k))
+        vp = F.pad(vc, (0, w - vc.shape[-1])) if w > vc.shape[-1] else vc
+        outs.append(flash_attn_forward(qp, kp, vp, scale=scale, causal=causal)[..., :vc.shape[-1]])
+    return outs[0] if len(outs) == 1 else torch.cat(outs, dim=-1)
+
+
 def _sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None, **kwargs):
     eligible, _ = _eligibility(query, key, value, attn_mask, dropout_p, is_causal)
     if eligible:
         try:
             s = scale if scale is not None else 1.0 / math.sqrt(query.shape[-1])
+            if value.shape[-1] != query.shape[-1]:
+                return _uneven_v(query, key, value, s, is_causal)
             return flash_attn_forward(query, key, value, scale=s, causal=is_causal)
         except Exception as e:  # never crash: fall back to stock SDPA
             print(f"[mtlflashattn_amd/sdpa] kernel fell back ({e}); using stock SDPA")
@@ -124,7 +152,7 @@ def install(min_score_gb=None, min_seq=None, fast_min_seq=None):
     if min_seq is None:
         min_seq = int(os.environ.get("MTLFLASHATTN_SDPA_MIN_SEQ", "4096"))
     if fast_min_seq is None:
-        fast_min_seq = int(os.environ.get("MTLFLASHATTN_SDPA_FAST_MIN_SEQ", "1024"))
+        fast_min_seq = int(os.environ.get("MTLFLASHATTN_SDPA_FAST_MIN_SEQ", "512"))
     _min_score_bytes = int(min_score_gb * (1024 ** 3))
     _min_seq = min_seq
     _fast_min_seq = fast_min_seq

@@ -17,6 +17,11 @@ Follows, step for step:
   * metal_flash_attn/__init__.py:62-99 (heads-third API, default scale
     1/sqrt(D)) and :102-183 (varlen: one B=1 call per sequence, empty query
     sequences skipped, [B, Hq] ALiBi rows picked per sequence).
+  * metal_flash_attn/sdpa.py:86-130 (`_uneven_v_attention`, the exact path of
+    the SDPA patch for value head dim != query/key head dim): GQA expansion
+    only with enable_gqa, fp32 scores in query chunks, bool / additive masks,
+    TOP-LEFT causal (torch SDPA's convention), nan_to_num, @ V, cast to V's
+    dtype (`uneven_v_attention`).
 
 Pinned by tests/test_oracle_pinning.py against torch's SDPA (a library
 routine), an independent float64 C restatement of the streaming kernel
@@ -137,3 +142,40 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=No
                         scale, causal, softcap, window_size[0], window_size[1], alibi, chunk=chunk)
         out[cu_q[i]:cu_q[i + 1]] = o[0].permute(1, 0, 2)
     return out
+
+
+def uneven_v_attention(query, key, value, attn_mask=None, is_causal=False, scale=None, enable_gqa=False,
+                       q_chunk=4096):
+    """[B, H, L, D] SDPA semantics with value head dim Dv != D (sdpa.py:86-130).
+
+    Returns [B, Hq, Lq, Dv] in value.dtype.  Causal is top-left aligned (key j
+    visible to query i iff j <= i), as in torch SDPA."""
+    Hq, Hkv = query.shape[1], key.shape[1]
+    if Hq != Hkv:
+        if not (enable_gqa and Hkv != 0 and Hq % Hkv == 0):
+            raise ValueError(f"SDPA query/kv head mismatch (Hq={Hq}, Hkv={Hkv}); pass enable_gqa=True")
+        key = key.repeat_interleave(Hq // Hkv, dim=1)
+        value = value.repeat_interleave(Hq // Hkv, dim=1)
+    s = scale if scale is not None else 1.0 / math.sqrt(query.shape[-1])
+    Lq, Lk = query.shape[-2], key.shape[-2]
+    bias = None
+    if attn_mask is not None:
+        if attn_mask.dtype == torch.bool:
+            bias = torch.zeros(attn_mask.shape, dtype=torch.float32).masked_fill(~attn_mask.cpu(), float("-inf"))
+        else:
+            bias = attn_mask.detach().cpu().float()
+    key_t = key.detach().cpu().float().transpose(-2, -1)
+    value_f = value.detach().cpu().float()
+    outs = []
+    for i in range(0, Lq, q_chunk):
+        qi = query[..., i:i + q_chunk, :].detach().cpu().float()
+        scores = torch.matmul(qi, key_t) * s
+        if bias is not None:
+            scores = scores + (bias[..., i:i + qi.shape[-2], :] if bias.shape[-2] == Lq else bias)
+        if is_causal:
+            qpos = torch.arange(i, i + qi.shape[-2]).unsqueeze(-1)
+            kpos = torch.arange(Lk).unsqueeze(0)
+            scores = scores.masked_fill(kpos > qpos, float("-inf"))
+        probs = torch.nan_to_num(scores.softmax(dim=-1), nan=0.0)
+        outs.append(torch.matmul(probs, value_f))
+    return torch.cat(outs, dim=-2).to(value.dtype)

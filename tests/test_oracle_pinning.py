@@ -296,3 +296,46 @@ def test_alibi_broadcast_shapes():
     assert torch.equal(chunked.broadcast_alibi(bh, 3, 2), torch.arange(6.0))
     with pytest.raises(ValueError):
         chunked.broadcast_alibi(torch.ones(3), 3, 2)
+
+
+# ---- uneven value head dim (the reference SDPA patch's exact path) ----------
+
+@pytest.mark.parametrize("d,dv", [(64, 32), (64, 128), (32, 200)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_uneven_v_matches_sdpa(d, dv, causal):
+    g = torch.Generator().manual_seed(d + dv)
+    q = torch.randn(2, 3, 40, d, generator=g)
+    k = torch.randn(2, 3, 40, d, generator=g)
+    v = torch.randn(2, 3, 40, dv, generator=g)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+    out = chunked.uneven_v_attention(q, k, v, is_causal=causal)
+    assert out.shape == (2, 3, 40, dv)
+    assert (out - ref).abs().max() < 2e-6
+
+
+def test_uneven_v_top_left_causal_cross_length_and_masks():
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, 2, 24, 16, generator=g)
+    k = torch.randn(1, 2, 56, 16, generator=g)
+    v = torch.randn(1, 2, 56, 48, generator=g)
+    # top-left causal: query i sees keys 0..i (torch SDPA's convention)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    assert (chunked.uneven_v_attention(q, k, v, is_causal=True) - ref).abs().max() < 2e-6
+    mask = torch.rand(24, 56, generator=g) > 0.3
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    assert (chunked.uneven_v_attention(q, k, v, attn_mask=mask) - ref).abs().max() < 2e-6
+    add = torch.randn(24, 56, generator=g)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=add)
+    assert (chunked.uneven_v_attention(q, k, v, attn_mask=add) - ref).abs().max() < 2e-6
+
+
+def test_uneven_v_single_key_and_gqa():
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(1, 4, 5, 16, generator=g)
+    k = torch.randn(1, 2, 1, 16, generator=g)
+    v = torch.randn(1, 2, 1, 40, generator=g)
+    out = chunked.uneven_v_attention(q, k, v, enable_gqa=True)
+    # one key: every query gets that key's value row (its kv head's)
+    assert torch.allclose(out, v.repeat_interleave(2, dim=1).expand(1, 4, 5, 40), atol=0)
+    with pytest.raises(ValueError):
+        chunked.uneven_v_attention(q, k, v)  # Hq != Hkv without enable_gqa

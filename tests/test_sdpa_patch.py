@@ -79,6 +79,37 @@ class TestGates:
         finally:
             sdpa.uninstall()
 
+    def test_rocm_derived_fast_floor_and_tiers(self):
+        # fp16/bf16 from 512 tokens, fp32 too (measured against stock ROCm SDPA)
+        assert sdpa.install()
+        try:
+            for dt in (torch.float16, torch.bfloat16, torch.float32):
+                q = torch.zeros(1, 2, 512, 64, dtype=dt)
+                assert self.elig(q, q, q) == (True, "fast-tier"), dt
+                q = torch.zeros(1, 2, 511, 64, dtype=dt)
+                assert self.elig(q, q, q)[1].startswith("fits"), dt
+            # head dim not a multiple of 8 (padded copies): only the other gates
+            q = torch.zeros(1, 2, 1024, 100, dtype=torch.float16)
+            assert self.elig(q, q, q)[1].startswith("fits")
+        finally:
+            sdpa.uninstall()
+
+    def test_uneven_value_head_dim_is_eligible(self):
+        q = torch.zeros(1, 2, 1024, 64, dtype=torch.float16)
+        assert sdpa.install()
+        try:
+            for dv in (32, 128, 200, 256):
+                v = torch.zeros(1, 2, 1024, dv, dtype=torch.float16)
+                assert self.elig(q, q, v) == (True, "fast-tier"), dv
+            v = torch.zeros(1, 2, 1024, 128, dtype=torch.float16)
+            assert self.elig(q, q, v, mask=torch.zeros(1024, 1024)) == (False, "attn_mask")
+            k = torch.zeros(1, 2, 1000, 64, dtype=torch.float16)
+            assert self.elig(q, k, v[:, :, :1000], causal=True) == (False, "causal-cross-length")
+            big = torch.zeros(1, 2, 1024, 160, dtype=torch.float16)
+            assert self.elig(big, big, v)[1].startswith("head_dim")
+        finally:
+            sdpa.uninstall()
+
     def test_tiny_stays_stock(self):
         q = torch.zeros(1, 2, 64, 64, dtype=torch.float16)
         assert sdpa.install()
@@ -97,7 +128,7 @@ class TestGates:
             sdpa.uninstall()
 
     def test_env_configurable_floors(self, monkeypatch):
-        q = torch.zeros(1, 2, 512, 64, dtype=torch.float16)
+        q = torch.zeros(1, 2, 300, 64, dtype=torch.float16)
         monkeypatch.setenv("MTLFLASHATTN_SDPA_FAST_MIN_SEQ", "256")
         assert sdpa.install()
         try:
@@ -183,5 +214,35 @@ class TestSdpaOnGpu:
         q, k, v = self.make(1, 2, 64, 64, 64)
         mask = torch.zeros(64, 64, device="cuda", dtype=torch.float16)
         mask[:, 32:] = float("-inf")
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        assert torch.equal(out, patched._orig(q, k, v, attn_mask=mask))
+
+    @pytest.mark.parametrize("d,dv", [(128, 64), (64, 128), (64, 200), (40, 96)])
+    @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+    def test_uneven_value_head_dim_on_the_kernel(self, patched, monkeypatch, d, dv, dtype):
+        from oracle import chunked
+
+        calls = []
+        orig = sdpa.flash_attn_forward
+        monkeypatch.setattr(sdpa, "flash_attn_forward", lambda *a, **kw: calls.append(1) or orig(*a, **kw))
+        g = torch.Generator().manual_seed(d + dv)
+        q = torch.randn(1, 8, 96, d, generator=g).to("cuda", dtype)
+        k = torch.randn(1, 2, 96, d, generator=g).to("cuda", dtype)
+        v = torch.randn(1, 2, 96, dv, generator=g).to("cuda", dtype)
+        for causal in (False, True):
+            calls.clear()
+            out = F.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True)
+            assert calls, "uneven-V call did not reach the HIP kernel"
+            assert len(calls) == -(-dv // 128)  # one launch per 128 value columns
+            assert out.shape == (1, 8, 96, dv) and out.dtype == dtype
+            ref = chunked.uneven_v_attention(q.float(), k.float(), v.float(), is_causal=causal, enable_gqa=True)
+            err = (out.float().cpu() - ref).abs().max().item()
+            bar = 1e-5 if dtype == torch.float32 else 4e-3 * ref.abs().max().item()
+            assert err <= bar, f"D={d} Dv={dv} causal={causal}: err {err:.3e} > {bar:.3e}"
+
+    def test_uneven_value_head_dim_with_mask_stays_stock(self, patched):
+        q, k, _ = self.make(1, 2, 64, 64, 64)
+        v = torch.randn(1, 2, 64, 96, device="cuda", dtype=torch.float16)
+        mask = torch.zeros(64, 64, device="cuda", dtype=torch.float16)
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
         assert torch.equal(out, patched._orig(q, k, v, attn_mask=mask))
