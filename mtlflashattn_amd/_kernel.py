@@ -186,6 +186,29 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
         return out.zero_()  # no keys: every row is fully masked -> 0
 
     Dp = -(-D // 8) * 8
+    if Dp == D:
+        # fast path: tensors used in place; the launch parameters of this
+        # signature (everything but the data pointers) are prepared once
+        key = (q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), out.shape, out.stride(), q.dtype,
+               out.dtype, q.device.index, float(scale), bool(causal), float(softcap), int(window_left),
+               int(window_right), alibi is not None, alibi_bstride,
+               (cu_q.shape[0], Lq, Lk) if varlen else None, _TILE_HINT, _SPLIT_KEYS)
+        ent = _plans.get(key)
+        if ent is None and all(_fits_strides(t) for t in (q, k, v, out)):
+            ent = _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, softcap, window_left,
+                           window_right, alibi is not None, alibi_bstride)
+            if len(_plans) >= _PLANS_MAX:
+                _plans.clear()
+            _plans[key] = ent
+        if ent is not None and not ((q.data_ptr() | k.data_ptr() | v.data_ptr() | out.data_ptr()) & 15):
+            p = _hip.MfaFwdParams.from_buffer_copy(ent[0])
+            p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+            if varlen:
+                p.cu_seqlens_q, p.cu_seqlens_k = cu_q.data_ptr(), cu_k.data_ptr()
+            if alibi is not None:
+                p.alibi_slopes = alibi.data_ptr()
+            _launch(p, ent[1], q.device)
+            return out
     if Dp != D:  # the kernels read 16-byte chunks: zero-pad the head dim
         q, k, v = (F.pad(t, (0, Dp - D)) for t in (q, k, v))
     q, k, v = (t if _fits_abi(t) else t.contiguous() for t in (q, k, v))
@@ -216,22 +239,74 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and Dp > 64):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
-    chunk = 0
-    if q.dtype != torch.float32 and hint != _hip.MFA_TILE_PINGPONG:
-        chunk = _hip.split_keys(p) if _SPLIT_KEYS is None else _SPLIT_KEYS
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        if chunk:
-            # split-KV: partials in a workspace from torch's stream-ordered
-            # caching allocator (reused only after these kernels ran)
-            nbytes = _hip.workspace_bytes(p, chunk)
-            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-            _hip.fwd_splitkv(p, chunk, ws.data_ptr(), nbytes, stream)
-        else:
-            _hip.fwd(p, stream)
+    _launch(p, _split_choice(p, q.dtype, hint), q.device)
     if dst is not out:
         out.copy_(dst[..., :D])
     return out
+
+
+# prepared launch parameters per call signature (see _run's fast path)
+_plans = {}
+_PLANS_MAX = 512
+
+
+def _fits_strides(x: torch.Tensor) -> bool:
+    """_fits_abi without the base-address test (strides only)."""
+    if x.stride(-1) != 1 and x.shape[-1] > 1:
+        return False
+    al = 16 // x.element_size()
+    return all(st % al == 0 for st, n in zip(x.stride()[:-1], x.shape[:-1]) if n > 1)
+
+
+def _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, softcap, window_left, window_right,
+             has_alibi, alibi_bstride):
+    """(parameter template without data pointers, split-KV choice) of a call."""
+    p = _hip.MfaFwdParams()
+    p.q_batch_stride, p.q_seq_stride, p.q_head_stride = _strides_bsh(q)
+    p.k_batch_stride, p.k_seq_stride, p.k_head_stride = _strides_bsh(k)
+    p.v_batch_stride, p.v_seq_stride, p.v_head_stride = _strides_bsh(v)
+    p.o_batch_stride, p.o_seq_stride, p.o_head_stride = _strides_bsh(out)
+    p.batch, p.heads_q, p.heads_kv = batch, Hq, Hkv
+    p.seqlen_q, p.seqlen_k, p.head_dim = Lq, Lk, Dp
+    if varlen:  # placeholders: the choice below only needs to see varlen
+        p.cu_seqlens_q = p.cu_seqlens_k = 256
+    p.scale, p.softcap = float(scale), float(softcap)
+    p.window_left, p.window_right = int(window_left), int(window_right)
+    p.causal = 1 if causal else 0
+    if has_alibi:
+        p.alibi_slopes = 256
+        p.alibi_batch_stride = alibi_bstride
+    p.dtype_in = _hip.DTYPE_CODES[q.dtype]
+    p.dtype_out = _hip.DTYPE_CODES[out.dtype]
+    hint = _TILE_HINT
+    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and Dp > 64):
+        hint = _hip.MFA_TILE_AUTO
+    p.tile_hint = hint
+    chunk = _split_choice(p, q.dtype, hint)
+    p.cu_seqlens_q = p.cu_seqlens_k = p.alibi_slopes = None
+    return p, chunk
+
+
+def _split_choice(p, dtype, hint):
+    if dtype == torch.float32 or hint == _hip.MFA_TILE_PINGPONG:
+        return 0
+    return _hip.split_keys(p) if _SPLIT_KEYS is None else _SPLIT_KEYS
+
+
+def _launch(p, chunk, device):
+    idx = device.index
+    if idx != torch.cuda.current_device():
+        with torch.cuda.device(device):
+            return _launch(p, chunk, device)
+    stream = torch._C._cuda_getCurrentRawStream(idx)
+    if chunk:
+        # split-KV: partials in a workspace from torch's stream-ordered
+        # caching allocator (reused only after these kernels ran)
+        nbytes = _hip.workspace_bytes(p, chunk)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _hip.fwd_splitkv(p, chunk, ws.data_ptr(), nbytes, stream)
+    else:
+        _hip.fwd(p, stream)
 
 
 def _out_dtype(q, out_dtype):

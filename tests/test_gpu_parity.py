@@ -57,6 +57,19 @@ def test_native_library_is_the_path():
     assert native_library_mapped(), "libmtlfa_hip.so is not mapped: the HIP path did not run"
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_launch_parameter_reuse(dtype):
+    # V with strides unlike K's (prepared parameters are per signature) and a
+    # second call of the same signature on new data
+    q, k, v = make_qkv(2, 64, 80, 4, 4, 64, dtype, seed=1)
+    v2 = v.transpose(1, 2).contiguous().transpose(1, 2)
+    assert v2.stride() != v.stride()
+    assert torch.equal(mfa.flash_attn_func(q, k, v2), mfa.flash_attn_func(q, k, v))
+    q, k, v = make_qkv(2, 64, 80, 4, 4, 64, dtype, seed=2)
+    check(q, k, v, "second call of one signature")
+    check(q, k, v.transpose(1, 2).contiguous().transpose(1, 2), "second call, strided V")
+
+
 def test_config1_fp32_exact_inputs():
     # B=1, L=512, H=2, D=64, fp32, non-causal, scale 1/8, seed 0
     q, k, v = make_qkv(1, 512, 512, 2, 2, 64, torch.float32, seed=0)
