@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MFA_ABI_VERSION 2
+#define MFA_ABI_VERSION 3
 
 /* element types (dtype_in / dtype_out) */
 #define MFA_DTYPE_F16 0
@@ -115,6 +115,35 @@ typedef struct mfa_fwd_params {
     int32_t dtype_out; /* == dtype_in, or MFA_DTYPE_F32 (full-precision output) */
     int32_t tile_hint; /* MFA_TILE_AUTO (0); the others force a bf16/fp16 kernel
                           (tests and tuning; results are the same either way) */
+
+    /* Softmax log-sum-exp output (optional; the reference raises for it,
+     * metal_flash_attn/__init__.py:49-50).  lse = ln(sum_j exp(s_j)) over the
+     * row's valid keys, s the transformed score above (natural-log units, as
+     * CUDA flash-attn's softmax_lse), -inf for a row with no valid key.  fp32,
+     * query rows contiguous: dense lse[b * lse_batch_stride + h *
+     * lse_head_stride + i]; varlen lse[h * lse_head_stride + cu_seqlens_q[b]
+     * + i] (lse_batch_stride ignored; [heads_q, total_q] when
+     * lse_head_stride = total_q). */
+    float* softmax_lse; /* NULL = not written */
+    int64_t lse_batch_stride;
+    int64_t lse_head_stride;
+
+    /* Paged K/V (optional; the reference raises for block_table,
+     * metal_flash_attn/__init__.py:130-131).  k and v are
+     * [num_pages, page_block_size, heads_kv, head_dim] addressed through
+     * k_batch_stride/v_batch_stride (page stride), *_seq_stride and
+     * *_head_stride; key j of sequence b is row j % page_block_size of page
+     * block_table[b * block_table_batch_stride + j / page_block_size].  The
+     * key count of sequence b is seqlen_k (dense) or cu_seqlens_k[b+1] -
+     * cu_seqlens_k[b] (varlen; the start offsets are not used for k/v).
+     * page_block_size is a positive multiple of 256; a page id outside
+     * [0, num_pages) reads as zeros (callers validate their tables).  Paged
+     * calls run on the 256-row and fp32 kernels: MFA_TILE_PINGPONG with a
+     * block_table is MFA_ERR_UNSUPPORTED. */
+    const int32_t* block_table; /* NULL = contiguous k/v */
+    int64_t block_table_batch_stride;
+    int32_t page_block_size;
+    int32_t num_pages;
 } mfa_fwd_params;
 
 /* Launch geometry of one mfa_fwd call (for profiling/roofline reports). */
@@ -175,7 +204,8 @@ int mfa_params_size(void);
  * mfa_fwd_splitkv: enqueue both kernels on `stream`; `workspace` is a
  * 256-byte aligned device buffer of at least that many bytes, owned by the
  * caller and reused only after the call's kernels ran (stream order).
- * split_keys must be 0 (same as mfa_fwd) or a positive multiple of 64. */
+ * split_keys must be 0 (same as mfa_fwd) or a positive multiple of 64 (of
+ * 256 with a block_table).  softmax_lse and block_table work as in mfa_fwd. */
 int32_t mfa_fwd_split_keys(const mfa_fwd_params* params);
 int64_t mfa_fwd_workspace_bytes(const mfa_fwd_params* params, int32_t split_keys);
 int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* workspace, int64_t workspace_bytes,

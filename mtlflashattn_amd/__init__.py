@@ -5,6 +5,12 @@ six functions, argument meanings and error contract.  Inference-only (no
 backward).  Unsupported features raise NotImplementedError so callers can fall
 back, rather than silently approximating (metal_flash_attn/__init__.py:1-5).
 
+Two additions the reference raises for: `flash_attn_varlen_func` accepts a
+paged K/V cache (`block_table`, CUDA flash-attn's layout), and
+`flash_attn_func_with_lse` / `flash_attn_varlen_func_with_lse` also return the
+softmax log-sum-exp, which `merge_attention_partials` uses to combine attention
+over disjoint key sets (context-parallel shards, cache + new tokens).
+
 Every call runs the gfx950 HIP kernels of libmtlfa_hip.so on the tensors'
 ROCm device; there is no CPU path.
 """
@@ -26,6 +32,9 @@ __all__ = [
     "flash_attn_varlen_qkvpacked_func",
     "flash_attn_varlen_kvpacked_func",
     "flash_attn_forward",
+    "flash_attn_func_with_lse",
+    "flash_attn_varlen_func_with_lse",
+    "merge_attention_partials",
     "__version__",
 ]
 
@@ -83,6 +92,25 @@ def flash_attn_func(
     Hkv must divide Hq (GQA/MQA). Returns [B, Lq, Hq, D] in q.dtype.
     """
     _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, deterministic, return_attn_probs)
+    return _dense(q, k, v, softmax_scale, causal, window_size, softcap, alibi_slopes, False)
+
+
+def flash_attn_func_with_lse(q, k, v, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                             alibi_slopes=None):
+    """flash_attn_func that also returns the softmax log-sum-exp.
+
+    Returns (out [B, Lq, Hq, D] in q.dtype, softmax_lse [B, Hq, Lq] fp32):
+    lse = ln(sum_j exp(s_j)) over each row's valid keys (s the scaled,
+    soft-capped, ALiBi-biased score; CUDA flash-attn's softmax_lse), -inf for a
+    row with no valid key.  Same arguments and errors as flash_attn_func; the
+    reference has no counterpart (its return_attn_probs raises,
+    metal_flash_attn/__init__.py:49-50).
+    """
+    _check_supported(q, k, v, 0.0, window_size, softcap, alibi_slopes, False, False)
+    return _dense(q, k, v, softmax_scale, causal, window_size, softcap, alibi_slopes, True)
+
+
+def _dense(q, k, v, softmax_scale, causal, window_size, softcap, alibi_slopes, return_lse):
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError(f"mtlflashattn_amd: expected 4-D [B,S,H,D] tensors, got q.dim()={q.dim()}")
     Hq, Hkv = q.shape[2], k.shape[2]
@@ -93,7 +121,7 @@ def flash_attn_func(
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     return forward_bshd(
         q, k, v, scale=scale, causal=causal, softcap=softcap,
-        window_left=window_size[0], window_right=window_size[1], alibi_slopes=alibi_slopes,
+        window_left=window_size[0], window_right=window_size[1], alibi_slopes=alibi_slopes, return_lse=return_lse,
     )
 
 
@@ -120,22 +148,59 @@ def flash_attn_varlen_func(
     q: [total_q, Hq, D]; k, v: [total_k, Hkv, D] packed without padding;
     cu_seqlens_*: [B+1] int32 cumulative sequence lengths.
     Returns [total_q, Hq, D] in q.dtype.  All sequences run in one launch.
+
+    block_table (paged K/V cache, CUDA flash-attn's layout; the reference
+    raises NotImplementedError, metal_flash_attn/__init__.py:130-131): int32
+    [B, max_pages]; k, v are then page pools [num_pages, page_block_size, Hkv,
+    D] with page_block_size a multiple of 256, key j of sequence b is row
+    j % page_block_size of page block_table[b, j // page_block_size], and
+    cu_seqlens_k gives the key counts only.
     """
     _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, deterministic, return_attn_probs)
-    if block_table is not None:
-        raise NotImplementedError("mtlflashattn_amd: block_table (paged KV cache) not supported")
-    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+    return _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_size, softcap, alibi_slopes,
+                   block_table, False)
+
+
+def flash_attn_varlen_func_with_lse(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                    softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                                    alibi_slopes=None, block_table=None):
+    """flash_attn_varlen_func that also returns the softmax log-sum-exp.
+
+    Returns (out [total_q, Hq, D] in q.dtype, softmax_lse [Hq, total_q] fp32,
+    CUDA flash-attn's varlen layout); lse as in flash_attn_func_with_lse.
+    """
+    _check_supported(q, k, v, 0.0, window_size, softcap, alibi_slopes, False, False)
+    return _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_size, softcap, alibi_slopes,
+                   block_table, True)
+
+
+def _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_size, softcap, alibi_slopes,
+            block_table, return_lse):
+    paged = block_table is not None
+    if q.dim() != 3 or k.dim() != (4 if paged else 3) or v.dim() != (4 if paged else 3):
+        if paged:
+            raise ValueError("mtlflashattn_amd: with block_table, q must be [total,H,D] and k/v "
+                             "[num_pages,page_block_size,H,D]")
         raise ValueError(f"mtlflashattn_amd: expected 3-D [total,H,D] tensors, got q.dim()={q.dim()}")
     if cu_seqlens_q.shape[0] != cu_seqlens_k.shape[0]:
         raise ValueError(
             f"mtlflashattn_amd: cu_seqlens_q ({cu_seqlens_q.shape[0]}) and "
             f"cu_seqlens_k ({cu_seqlens_k.shape[0]}) imply different batch sizes"
         )
-    Hq, Hkv = q.shape[1], k.shape[1]
+    Hq, Hkv = q.shape[1], k.shape[-2]
     if Hkv == 0 or Hq % Hkv != 0:
         raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
-    if k.shape[0] != v.shape[0]:
+    if k.shape[:-1] != v.shape[:-1]:
         raise ValueError("mtlflashattn_amd: k/v total token count mismatch")
+    if paged:
+        page = k.shape[1]
+        if not torch.is_tensor(block_table) or block_table.dim() != 2 or block_table.dtype != torch.int32:
+            raise ValueError("mtlflashattn_amd: block_table must be an int32 [batch, max_pages] tensor")
+        if block_table.shape[0] != cu_seqlens_q.shape[0] - 1:
+            raise ValueError(f"mtlflashattn_amd: block_table has {block_table.shape[0]} rows for "
+                             f"{cu_seqlens_q.shape[0] - 1} sequences")
+        if page == 0 or page % 256 != 0:
+            raise ValueError(f"mtlflashattn_amd: page_block_size {page} must be a positive multiple of 256")
 
     # One host read of both prefix sums (the reference reads them for the same
     # checks, metal_flash_attn/__init__.py:145-154); it also yields the true
@@ -145,19 +210,59 @@ def flash_attn_varlen_func(
     cu_q, cu_k = cu[:n], cu[n:]
     if cu_q[-1] != q.shape[0]:
         raise ValueError(f"mtlflashattn_amd: cu_seqlens_q[-1]={cu_q[-1]} != total_q={q.shape[0]}")
-    if cu_k[-1] != k.shape[0]:
+    if not paged and cu_k[-1] != k.shape[0]:
         raise ValueError(f"mtlflashattn_amd: cu_seqlens_k[-1]={cu_k[-1]} != total_k={k.shape[0]}")
     lens_q = [b - a for a, b in zip(cu_q[:-1], cu_q[1:])]
     lens_k = [b - a for a, b in zip(cu_k[:-1], cu_k[1:])]
     if any(x < 0 for x in lens_q) or any(x < 0 for x in lens_k) or cu_q[0] != 0 or cu_k[0] != 0:
         raise ValueError("mtlflashattn_amd: cu_seqlens must be non-decreasing prefix sums starting at 0")
+    if paged:
+        _check_block_table(block_table, lens_k, k.shape[1], k.shape[0])
 
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     return forward_varlen(
         q, k, v, cu_seqlens_q, cu_seqlens_k, max(lens_q, default=0), max(lens_k, default=0),
         scale=scale, causal=causal, softcap=softcap, window_left=window_size[0],
-        window_right=window_size[1], alibi_slopes=alibi_slopes,
+        window_right=window_size[1], alibi_slopes=alibi_slopes, return_lse=return_lse, block_table=block_table,
     )
+
+
+def _check_block_table(block_table, lens_k, page, num_pages):
+    """Every page a sequence uses must exist (one host read of the table)."""
+    need = [-(-n // page) for n in lens_k]
+    if max(need, default=0) > block_table.shape[1]:
+        raise ValueError(f"mtlflashattn_amd: block_table has {block_table.shape[1]} pages per sequence, "
+                         f"{max(need)} needed for {max(lens_k)} keys")
+    if not need or max(need) == 0:
+        return
+    used = torch.arange(block_table.shape[1]).unsqueeze(0) < torch.tensor(need).unsqueeze(1)
+    ids = block_table.cpu()[used]
+    if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= num_pages):
+        raise ValueError(f"mtlflashattn_amd: block_table holds page ids outside [0, {num_pages})")
+
+
+def merge_attention_partials(outs, lses):
+    """Combine attentions of the same queries over disjoint key sets.
+
+    outs: list of [..., Lq, Hq, D] outputs (any float dtype), lses: the
+    matching [..., Hq, Lq] fp32 log-sum-exps (flash_attn_func_with_lse
+    layout).  Returns (out in outs[0].dtype, lse): out = sum_i w_i out_i with
+    w_i = exp(lse_i - lse), lse = ln(sum_i exp(lse_i)); rows without a valid
+    key in any part get out = 0, lse = -inf.  This is the merge a
+    context-parallel forward (key/value shards on different GPUs) or a
+    cache + new-token split needs; it runs as PyTorch elementwise ops.
+    """
+    if len(outs) != len(lses) or not outs:
+        raise ValueError("mtlflashattn_amd: merge_attention_partials needs matching, non-empty outs and lses")
+    lse_all = torch.stack([x.float() for x in lses])
+    lse = torch.logsumexp(lse_all, dim=0)
+    safe = torch.where(torch.isinf(lse), torch.zeros_like(lse), lse)
+    acc = None
+    for o, l in zip(outs, lse_all):
+        w = torch.exp(l - safe).masked_fill(torch.isinf(lse), 0.0)
+        term = o.float() * w.transpose(-1, -2).unsqueeze(-1)
+        acc = term if acc is None else acc + term
+    return acc.to(outs[0].dtype), lse
 
 
 def flash_attn_qkvpacked_func(qkv, *args, **kwargs):

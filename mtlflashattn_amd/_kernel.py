@@ -45,7 +45,8 @@ _warned_modes = set()
 
 # Preferred C-ABI tile_hint for bf16/fp16 launches (0 = the library's choice);
 # tests set it to run every case through each kernel.  A preference the launch
-# cannot take (fp32, ping-pong with a head dim above 64) falls back to 0.
+# cannot take (fp32; ping-pong with a head dim above 64 or a block table)
+# falls back to 0.
 _TILE_HINT = 0
 # Split-KV chunk in keys for bf16/fp16 calls: None = the library's choice
 # (mfa_fwd_split_keys), 0 = never split, a multiple of 64 = that chunk
@@ -166,12 +167,17 @@ def _strides_bsh(x: torch.Tensor):
 
 
 def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, alibi, alibi_bstride,
-         cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None):
+         cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None, lse=None, block_table=None):
     """Launch the HIP forward on [B, S, H, D] views q, k, v and write `out`.
 
     out: [B, Sq, Hq, D] tensor of q.dtype or float32 (full-precision output).
     Varlen: q/k/v/out are [1, total, H, D] views, cu_q/cu_k int32 device
     tensors, seqlen_q/seqlen_k the maximum per-sequence lengths.
+    lse: optional fp32 softmax log-sum-exp output with contiguous rows,
+    [B, Hq, Lq] (dense) or [Hq, total_q] (varlen).
+    block_table: optional int32 [batch, pages per sequence] page table; k/v
+    are then [num_pages, page_block_size, Hkv, D] and every sequence's key
+    count comes from seqlen_k (dense) or cu_k (varlen).
     """
     _kernel_mode()
     B, Sq, Hq, D = q.shape
@@ -179,11 +185,15 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     varlen = cu_q is not None
     batch = (cu_q.shape[0] - 1) if varlen else B
     Lq = int(seqlen_q) if varlen else Sq
-    Lk = int(seqlen_k) if varlen else k.shape[1]
+    Lk = int(seqlen_k) if (varlen or block_table is not None) else k.shape[1]
     if batch == 0 or Lq == 0 or Hq == 0 or out.numel() == 0:
         return out
     if k.shape[1] == 0 or Lk == 0:
+        if lse is not None:
+            lse.fill_(float("-inf"))  # log-sum-exp over no key
         return out.zero_()  # no keys: every row is fully masked -> 0
+    lse_strides = (0 if varlen else lse.stride(0), lse.stride(-2)) if lse is not None else None
+    paged = (int(block_table.stride(0)), k.shape[1], k.shape[0]) if block_table is not None else None
 
     Dp = -(-D // 8) * 8
     if Dp == D:
@@ -192,11 +202,11 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
         key = (q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), out.shape, out.stride(), q.dtype,
                out.dtype, q.device.index, float(scale), bool(causal), float(softcap), int(window_left),
                int(window_right), alibi is not None, alibi_bstride,
-               (cu_q.shape[0], Lq, Lk) if varlen else None, _TILE_HINT, _SPLIT_KEYS)
+               (cu_q.shape[0], Lq, Lk) if varlen else None, _TILE_HINT, _SPLIT_KEYS, lse_strides, paged)
         ent = _plans.get(key)
         if ent is None and all(_fits_strides(t) for t in (q, k, v, out)):
             ent = _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, softcap, window_left,
-                           window_right, alibi is not None, alibi_bstride)
+                           window_right, alibi is not None, alibi_bstride, lse_strides, paged)
             if len(_plans) >= _PLANS_MAX:
                 _plans.clear()
             _plans[key] = ent
@@ -207,6 +217,10 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
                 p.cu_seqlens_q, p.cu_seqlens_k = cu_q.data_ptr(), cu_k.data_ptr()
             if alibi is not None:
                 p.alibi_slopes = alibi.data_ptr()
+            if lse is not None:
+                p.softmax_lse = lse.data_ptr()
+            if paged is not None:
+                p.block_table = block_table.data_ptr()
             _launch(p, ent[1], q.device)
             return out
     if Dp != D:  # the kernels read 16-byte chunks: zero-pad the head dim
@@ -236,9 +250,15 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and Dp > 64):
+    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and (Dp > 64 or paged is not None)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
+    if lse is not None:
+        p.softmax_lse = lse.data_ptr()
+        p.lse_batch_stride, p.lse_head_stride = lse_strides
+    if paged is not None:
+        p.block_table = block_table.data_ptr()
+        p.block_table_batch_stride, p.page_block_size, p.num_pages = paged
     _launch(p, _split_choice(p, q.dtype, hint), q.device)
     if dst is not out:
         out.copy_(dst[..., :D])
@@ -259,7 +279,7 @@ def _fits_strides(x: torch.Tensor) -> bool:
 
 
 def _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, softcap, window_left, window_right,
-             has_alibi, alibi_bstride):
+             has_alibi, alibi_bstride, lse_strides=None, paged=None):
     """(parameter template without data pointers, split-KV choice) of a call."""
     p = _hip.MfaFwdParams()
     p.q_batch_stride, p.q_seq_stride, p.q_head_stride = _strides_bsh(q)
@@ -279,9 +299,13 @@ def _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, so
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and Dp > 64):
+    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and (Dp > 64 or paged is not None)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
+    if lse_strides is not None:
+        p.lse_batch_stride, p.lse_head_stride = lse_strides
+    if paged is not None:
+        p.block_table_batch_stride, p.page_block_size, p.num_pages = paged
     chunk = _split_choice(p, q.dtype, hint)
     p.cu_seqlens_q = p.cu_seqlens_k = p.alibi_slopes = None
     return p, chunk
@@ -318,12 +342,15 @@ def _out_dtype(q, out_dtype):
 
 
 def flash_attn_forward(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1,
-                       alibi_slopes=None, out_dtype=None):
+                       alibi_slopes=None, out_dtype=None, return_lse=False):
     """q: [B,Hq,Lq,D], k/v: [B,Hkv,Lk,D] (heads-second, any strides).
 
     Returns [B,Hq,Lq,D] contiguous, in q.dtype (metal_flash_attn/_kernel.py:1052-1056).
     out_dtype=torch.float32 returns the kernel's fp32 result before the
     final rounding to q.dtype (the parity mode for bf16/fp16 inputs).
+    return_lse=True returns (out, lse) with the fp32 softmax log-sum-exp
+    lse [B,Hq,Lq] (natural log, -inf for rows with no valid key); the
+    reference has no such output.
     """
     if _trace_enabled():
         _record_trace(q.dtype, q.shape[-1], q.shape[2], k.shape[2], causal)
@@ -341,19 +368,21 @@ def flash_attn_forward(q, k, v, scale, causal, softcap=0.0, window_left=-1, wind
     if D > MAX_HEAD_DIM:
         raise NotImplementedError(f"mtlflashattn_amd: head_dim {D} > {MAX_HEAD_DIM}")
     out = torch.empty(B, Hq, Lq, D, dtype=_out_dtype(q, out_dtype), device=q.device)
+    lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device) if return_lse else None
     _run(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2),
          scale=scale, causal=causal, softcap=softcap, window_left=window_left,
-         window_right=window_right, alibi=alibi, alibi_bstride=bstride)
-    return out
+         window_right=window_right, alibi=alibi, alibi_bstride=bstride, lse=lse)
+    return (out, lse) if return_lse else out
 
 
 def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1,
-                 alibi_slopes=None, out_dtype=None):
+                 alibi_slopes=None, out_dtype=None, return_lse=False):
     """Heads-third forward: q [B,Lq,Hq,D], k/v [B,Lk,Hkv,D] -> [B,Lq,Hq,D].
 
     Same result as flash_attn_forward on the transposed views followed by
     `.transpose(1, 2).contiguous()` (metal_flash_attn/__init__.py:93-99), but
     the kernel writes the heads-third output directly (no layout copies).
+    return_lse=True returns (out, lse [B,Hq,Lq] fp32).
     """
     if _trace_enabled():
         _record_trace(q.dtype, q.shape[-1], q.shape[1], k.shape[1], causal)
@@ -362,17 +391,22 @@ def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_rig
     B, Lq, Hq, D = q.shape
     alibi, bstride = _alibi_arg(alibi_slopes, B, Hq, q.device)
     out = torch.empty(B, Lq, Hq, D, dtype=_out_dtype(q, out_dtype), device=q.device)
-    return _run(q, k, v, out, scale=scale, causal=causal, softcap=softcap, window_left=window_left,
-                window_right=window_right, alibi=alibi, alibi_bstride=bstride)
+    lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    _run(q, k, v, out, scale=scale, causal=causal, softcap=softcap, window_left=window_left,
+         window_right=window_right, alibi=alibi, alibi_bstride=bstride, lse=lse)
+    return (out, lse) if return_lse else out
 
 
 def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0, window_left=-1,
-                   window_right=-1, alibi_slopes=None, out_dtype=None):
+                   window_right=-1, alibi_slopes=None, out_dtype=None, return_lse=False, block_table=None):
     """Packed varlen forward in ONE launch: q [Tq,Hq,D], k/v [Tk,Hkv,D].
 
     cu_q/cu_k: int32 [batch+1] device tensors; max_q/max_k: the longest
     sequence lengths.  Replaces the reference's per-sequence loop of B=1
     dispatches (metal_flash_attn/__init__.py:165-182) with the same result.
+    return_lse=True returns (out, lse [Hq, Tq] fp32).  block_table: int32
+    [batch, pages per sequence]; k/v are then a page pool
+    [num_pages, page_block_size, Hkv, D] and cu_k gives the key counts only.
     """
     batch = cu_q.shape[0] - 1
     Hq = q.shape[1]
@@ -385,11 +419,18 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
     if _trace_enabled():
         _record_trace(q.dtype, q.shape[-1], max_q, max_k, causal, "hip-varlen")
     out = torch.empty(q.shape, dtype=_out_dtype(q, out_dtype), device=q.device)
+    lse = torch.empty(Hq, q.shape[0], dtype=torch.float32, device=q.device) if return_lse else None
     cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
     cu_k = cu_k.to(device=q.device, dtype=torch.int32).contiguous()
-    return _run(q[None], k[None], v[None], out[None], scale=scale, causal=causal, softcap=softcap,
-                window_left=window_left, window_right=window_right, alibi=alibi, alibi_bstride=bstride,
-                cu_q=cu_q, cu_k=cu_k, seqlen_q=max_q, seqlen_k=max_k)[0]
+    if block_table is not None:
+        block_table = block_table.to(device=q.device, dtype=torch.int32)
+        if block_table.stride(1) != 1:
+            block_table = block_table.contiguous()
+    _run(q[None], k if block_table is not None else k[None], v if block_table is not None else v[None], out[None],
+         scale=scale, causal=causal, softcap=softcap, window_left=window_left, window_right=window_right,
+         alibi=alibi, alibi_bstride=bstride, cu_q=cu_q, cu_k=cu_k, seqlen_q=max_q, seqlen_k=max_k, lse=lse,
+         block_table=block_table)
+    return (out, lse) if return_lse else out
 
 
 def split_chunk(q, k):

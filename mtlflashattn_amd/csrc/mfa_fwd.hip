@@ -140,7 +140,22 @@ struct KArgs {
     int32_t ws_ld;    // floats per workspace O row (padded head dim)
     float* ws_o;      // [nsplit][U][Lq][ws_ld]
     float* ws_lse;    // [nsplit][U][Lq]
+    // softmax log-sum-exp output (natural log; NULL = off), rows contiguous
+    float* lse;
+    int64_t lse_b, lse_h;
+    // paged K/V: key j of sequence b is row j % page of page
+    // bt[b * bt_b + j / page]; j / page = umulhi(j, page_m) >> page_s.
+    // Contiguous K/V: bt = NULL, page_m = 0 (every key is in "page" 0, whose
+    // id comes from a one-entry zero table).
+    const int32_t* bt;
+    int64_t bt_b;
+    int32_t page, npages;
+    uint32_t page_m;
+    int32_t page_s;
 };
+
+// page table of contiguous K/V: one page with id 0
+__device__ const int32_t kNoPages[1] = {0};
 
 // ----------------------------------------------------------------------------
 // small device helpers
@@ -255,9 +270,11 @@ __device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int
 
 struct SeqView {
     const char* q;
-    const char* k;
+    const char* k;  // K/V of this head: sequence start, or page 0 when paged
     const char* v;
     char* o;
+    float* lse;            // this (sequence, head)'s softmax_lse row, or NULL
+    const int32_t* bt;     // this sequence's page table row (kNoPages: contiguous)
     int Lq, Lk;
 };
 
@@ -274,20 +291,49 @@ __device__ __forceinline__ SeqView seq_view(const KArgs& a, int b, int hq) {
         s.Lq = a.cu_q[b + 1] - q_start;
         s.Lk = a.cu_k[b + 1] - k_start;
         qo = (int64_t)q_start * a.qs;
-        ko = (int64_t)k_start;
+        ko = a.bt ? 0 : (int64_t)k_start;  // paged: pages come from the table
         s.q = a.q + (qo + (int64_t)hq * a.qh) * ES;
         s.k = a.k + (ko * a.ks + (int64_t)hkv * a.kh) * ES;
         s.v = a.v + (ko * a.vs + (int64_t)hkv * a.vh) * ES;
         s.o = a.o + ((int64_t)q_start * a.os + (int64_t)hq * a.oh) * OES;
+        s.lse = a.lse ? a.lse + (int64_t)hq * a.lse_h + q_start : nullptr;
     } else {
         s.Lq = a.Lq;
         s.Lk = a.Lk;
+        const int64_t kb = a.bt ? 0 : (int64_t)b;  // paged: batch stride = page stride
         s.q = a.q + ((int64_t)b * a.qb + (int64_t)hq * a.qh) * ES;
-        s.k = a.k + ((int64_t)b * a.kb + (int64_t)hkv * a.kh) * ES;
-        s.v = a.v + ((int64_t)b * a.vb + (int64_t)hkv * a.vh) * ES;
+        s.k = a.k + (kb * a.kb + (int64_t)hkv * a.kh) * ES;
+        s.v = a.v + (kb * a.vb + (int64_t)hkv * a.vh) * ES;
         s.o = a.o + ((int64_t)b * a.ob + (int64_t)hq * a.oh) * OES;
+        s.lse = a.lse ? a.lse + (int64_t)b * a.lse_b + (int64_t)hq * a.lse_h : nullptr;
     }
+    s.bt = a.bt ? a.bt + (int64_t)b * a.bt_b : kNoPages;
     return s;
+}
+
+// Element offset from sv.k (bstride = a.kb, sstride = a.ks) or sv.v of the
+// first row of the key block starting at key j, and whether that block may be
+// read.  Paged K/V: row j % page of page bt[j / page]; a block never straddles
+// pages (pages hold a multiple of 256 keys, blocks start at multiples of their
+// size, which divides 256).  The table index is clamped to the last key below
+// kend, so the prefetch of a block past the sequence reads no entry beyond the
+// sequence's own; a page id outside [0, npages) makes the block unreadable.
+// Contiguous K/V (PAGED false, a separate kernel instantiation): j * sstride,
+// with no table read -- the scalar load's wait (lgkmcnt) would also wait for
+// every LDS read in flight.  All values are wave-uniform, without branches.
+template <bool PAGED>
+__device__ __forceinline__ int64_t kv_block_off(const KArgs& a, const SeqView& sv, int j, int kend, int64_t bstride,
+                                                int64_t sstride, bool& ok) {
+    if constexpr (!PAGED) {
+        ok = true;
+        return (int64_t)j * sstride;
+    }
+    const uint32_t jj = (uint32_t)min(j, max(kend - 1, 0));
+    const int idx = (int)(__umulhi(jj, a.page_m) >> a.page_s);
+    // read-only during the kernel: a constant-address-space load (scalar unit)
+    const int pg = ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)sv.bt)[idx];
+    ok = (uint32_t)pg < (uint32_t)a.npages;
+    return (int64_t)(ok ? pg : 0) * bstride + (int64_t)(j - idx * a.page) * sstride;
 }
 
 // Valid key interval [lo, hi] of the query with bottom-right center `c`
@@ -479,10 +525,14 @@ __device__ __forceinline__ void qb_probs32(f32x16_t (&s)[NKB], float& l, float m
 }
 
 // Normalise and store O^T accumulators: lane (half, q) holds
-// d = 32*db + 8*g + 4*half + {0..3} for g = 0..3.
+// d = 32*db + 8*g + 4*half + {0..3} for g = 0..3.  With an lse output the
+// row's natural-log log-sum-exp (mu + log2 l) * ln 2 is stored too (the
+// probabilities were exp2(x*c - mu), l their sum), -inf for a row with no
+// valid key.
+constexpr float kLn2 = 0.6931471805599453f;
 template <int QB, int DB, bool IS_BF16>
 __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32x16_t (&o)[QB][DB],
-                                          const RowState (&rs)[QB], int qrow0, int lane) {
+                                          const RowState (&rs)[QB], int qrow0, int lane, float c) {
     const int l32 = lane & 31, half = lane >> 5;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -490,6 +540,10 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
         const float inv = l > 0.f ? 1.f / l : 0.f;  // fully masked rows -> 0 (_kernel.py:85)
         const int qrow = qrow0 + 32 * qb + l32;
         if (qrow >= sv.Lq) continue;
+        if (sv.lse && half == 0) {
+            const float mu = rs[qb].m == -INFINITY ? 0.f : rs[qb].m * c;
+            sv.lse[qrow] = l > 0.f ? (mu + __builtin_amdgcn_logf(l)) * kLn2 : -INFINITY;
+        }
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -546,7 +600,8 @@ __device__ __forceinline__ void store_partial(const KArgs& a, int Lq, int unit, 
     }
 }
 
-// Merge of the split-KV partials, one wavefront per query row.  A sequence
+// Merge of the split-KV partials, one wavefront per query row (and the
+// row's lse when requested: M + log2(sum_s w_s), in natural-log units).  A sequence
 // uses ceil(Lk / split_keys) chunks (one when it has no key); O =
 // sum_s w_s O_s / sum_s w_s with w_s = 2^(lse_s - M), M = max_s lse_s, and 0
 // when no chunk has a valid key (a fully masked row, _kernel.py:85-86).  The
@@ -579,6 +634,8 @@ __global__ void __launch_bounds__(64) mfa_combine_kernel(KArgs a) {
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) wsum += __shfl_xor(wsum, o);
+    if (sv.lse && lane == 0)  // natural-log lse of the merged row
+        sv.lse[qrow] = m == -INFINITY ? -INFINITY : (m + __builtin_amdgcn_logf(wsum)) * kLn2;
     __syncthreads();
     const int d = 2 * lane;
     if (d >= a.D) return;
@@ -614,7 +671,7 @@ __global__ void __launch_bounds__(64) mfa_combine_kernel(KArgs a) {
 // query block qb+1 and the PV MFMAs of query block qb-1 are interleaved with
 // the softmax VALU work of query block qb, so the matrix cores and the
 // vector ALU run concurrently within one wavefront.
-template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, bool PAGED>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MFA_WAVES_PER_EU)))
 mfa_fwd16_kernel(KArgs a) {
     constexpr int BM = kWaves * QB * 32;
@@ -736,13 +793,16 @@ mfa_fwd16_kernel(KArgs a) {
         // (computed without branches, so the pipelined block stays one basic block)
         const int rows = kend - j;
         const int rm1 = min(max(rows, 1), BN) - 1;
-        const int live = -(int)(rows > 0);
+        bool kok, vok;
+        const int64_t kbo = kv_block_off<PAGED>(a, sv, j, kend, a.kb, a.ks, kok);
+        const int64_t vbo = kv_block_off<PAGED>(a, sv, j, kend, a.vb, a.vs, vok);
+        const int live = -(int)(rows > 0 && kok && vok);
         const int kbytes = (int)(((int64_t)rm1 * a.ks + D) * 2) & live;
         const int vbytes = (int)(((int64_t)rm1 * a.vs + D) * 2) & live;
         const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(sv.k + (int64_t)j * a.ks * 2), (short)0, kbytes, kBufferDword3);
+            (void*)(sv.k + kbo * 2), (short)0, kbytes, kBufferDword3);
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(sv.v + (int64_t)j * a.vs * 2), (short)0, vbytes, kBufferDword3);
+            (void*)(sv.v + vbo * 2), (short)0, vbytes, kBufferDword3);
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
             kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
@@ -989,7 +1049,7 @@ mfa_fwd16_kernel(KArgs a) {
     if (a.nsplit > 1)
         store_partial<QB, DB>(a, Lq, b * a.Hq + hq, split, o, rs, c, wq0, lane);
     else
-        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
+        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
 }
 
 // ----------------------------------------------------------------------------
@@ -1104,7 +1164,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
     const int jbeg = (klo / BN) * BN;
     const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
     if (nblk == 0) {  // no valid key for any row of the tile: zeros
-        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
+        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
         return;
     }
 
@@ -1134,27 +1194,30 @@ mfa_fwd16_pp_kernel(KArgs a) {
     // host bounds the block span to 31 bits).
     const int kfull = ((BN - 1) * (int)a.ks + D) * 2;
     const int vfull = ((BN - 1) * (int)a.vs + D) * 2;
-    auto load_block = [&](const char* base, int64_t stride, int full, uint16_t* dst, uint32_t off, int u)
-        __attribute__((always_inline)) {
+    auto load_block = [&](const char* base, int64_t bstride, int64_t stride, int full, uint16_t* dst, uint32_t off,
+                          int u) __attribute__((always_inline)) {
         const int j = jbeg + u * BN;
         const int rows = Lk - j;
+        bool ok;
+        const int64_t bo = kv_block_off<false>(a, sv, j, Lk, bstride, stride, ok);
         int bytes = full;
         if (rows < BN) bytes = rows > 0 ? ((rows - 1) * (int)stride + D) * 2 : 0;
-        lds_load16(reinterpret_cast<uint64_t>(base + (int64_t)j * stride * 2), (uint32_t)bytes, dst, off);
+        if (!ok) bytes = 0;
+        lds_load16(reinterpret_cast<uint64_t>(base + bo * 2), (uint32_t)bytes, dst, off);
     };
     // loads of K block u into its stage u % NST (and likewise V); wave-uniform
     auto load_k = [&](int u) __attribute__((always_inline)) {
         if (loader) {
 #pragma unroll
             for (int i = 0; i < NL; ++i)
-                load_block(sv.k, a.ks, kfull, kst0 + (u % NST) * TILE + 512 * (wave + NW * i), kdoff[i], u);
+                load_block(sv.k, a.kb, a.ks, kfull, kst0 + (u % NST) * TILE + 512 * (wave + NW * i), kdoff[i], u);
         }
     };
     auto load_v = [&](int u) __attribute__((always_inline)) {
         if (loader) {
 #pragma unroll
             for (int i = 0; i < NL; ++i)
-                load_block(sv.v, a.vs, vfull, vst0 + (u % NST) * TILE + 512 * (wave + NW * i), vdoff[i], u);
+                load_block(sv.v, a.vb, a.vs, vfull, vst0 + (u % NST) * TILE + 512 * (wave + NW * i), vdoff[i], u);
         }
     };
     // Barrier at the end of phase p, once this wave's LDS reads have returned
@@ -1364,14 +1427,14 @@ mfa_fwd16_pp_kernel(KArgs a) {
         run(std::integral_constant<int, 1>{});
     // no direct-to-LDS write may land after the workgroup's LDS is released
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane);
+    store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
 }
 
 // ----------------------------------------------------------------------------
 // fp32 kernel: same structure with v_mfma_f32_32x32x2_f32.  K-slot layout of
 // the 32x32x2 MFMA: lane (half, x) supplies k = half, so QK^T step s uses
 // d = s + half*DP/2 and PV step r uses the key held in accumulator register r.
-template <int DP, int NKB, bool BIAS>
+template <int DP, int NKB, bool BIAS, bool PAGED>
 __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
     constexpr int QB = 1;
     constexpr int BM = kWaves * 32;
@@ -1447,15 +1510,18 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
 
     u32x4_t kreg[KCH], vreg[KCH];
     auto gload = [&](int j) {
+        bool kok, vok;
+        const int64_t kbo = kv_block_off<PAGED>(a, sv, j, Lk, a.kb, a.ks, kok);
+        const int64_t vbo = kv_block_off<PAGED>(a, sv, j, Lk, a.vb, a.vs, vok);
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
             const int cc = tid + kThreads * i;
             const int row = cc / CPR, col = (cc % CPR) * 4;
-            const bool ok = (cc < BN * CPR) && (j + row < Lk) && (col < D);
+            const bool ok = (cc < BN * CPR) && (j + row < Lk) && (col < D) && kok && vok;
             u32x4_t kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
             if (ok) {
-                kv = *reinterpret_cast<const u32x4_t*>(sv.k + ((int64_t)(j + row) * a.ks + col) * 4);
-                vv = *reinterpret_cast<const u32x4_t*>(sv.v + ((int64_t)(j + row) * a.vs + col) * 4);
+                kv = *reinterpret_cast<const u32x4_t*>(sv.k + (kbo + (int64_t)row * a.ks + col) * 4);
+                vv = *reinterpret_cast<const u32x4_t*>(sv.v + (vbo + (int64_t)row * a.vs + col) * 4);
             }
             kreg[i] = kv;
             vreg[i] = vv;
@@ -1530,7 +1596,7 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
     }
 
     // fp32 output (out_f32 is implied for fp32 input)
-    store_out<QB, DB, true>(a, sv, o, rs, wq0, lane);
+    store_out<QB, DB, true>(a, sv, o, rs, wq0, lane, c);
 }
 
 // ----------------------------------------------------------------------------
@@ -1558,10 +1624,12 @@ struct KernelCfg {
 };
 
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
-KernelCfg cfg16(const char* name) {
+KernelCfg cfg16(const char* name, bool paged) {
     constexpr int BM = kWaves * QB * 32, BN = NKB * 32;
     constexpr int kv = 2 * (BN * (DP + 8) + BN * (DP + MFA_V_PAD)), qs = BM * (DP + 8);
-    return KernelCfg{mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs), name};
+    return KernelCfg{paged ? (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, true>
+                           : (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, false>,
+                     BM, BN, 2 * (kv > qs ? kv : qs), name};
 }
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
 KernelCfg cfg16pp(const char* name) {
@@ -1571,10 +1639,12 @@ KernelCfg cfg16pp(const char* name) {
                      512};
 }
 template <int DP, int NKB, bool BIAS>
-KernelCfg cfg32(const char* name) {
+KernelCfg cfg32(const char* name, bool paged) {
     constexpr int BM = kWaves * 32, BN = NKB * 32;
     constexpr int kv = 2 * (BN * (DP + 4) + BN * (DP + 8)), qs = BM * (DP + 4);
-    return KernelCfg{mfa_fwd32_kernel<DP, NKB, BIAS>, BM, BN, 4 * (kv > qs ? kv : qs), name};
+    return KernelCfg{paged ? (kernel_fn)mfa_fwd32_kernel<DP, NKB, BIAS, true>
+                           : (kernel_fn)mfa_fwd32_kernel<DP, NKB, BIAS, false>,
+                     BM, BN, 4 * (kv > qs ? kv : qs), name};
 }
 
 // tile configuration per (dtype, padded head dim, bias)
@@ -1603,27 +1673,28 @@ KernelCfg cfg32(const char* name) {
 #ifndef MFA_PINGPONG
 #define MFA_PINGPONG 1
 #endif
+// paged K/V (block_table) runs on the 256-row and fp32 kernels only
 template <bool IS_BF16, bool BIAS>
-KernelCfg select16(int dp, bool fills_chip) {
+KernelCfg select16(int dp, bool fills_chip, bool paged) {
     if (MFA_PINGPONG && fills_chip && dp <= 64) {
         if (dp == 32)
             return cfg16pp<32, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,2,2>" : "mfa_fwd16pp<f16,d32,2,2>");
         return cfg16pp<64, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,2,2>" : "mfa_fwd16pp<f16,d64,2,2>");
     }
     switch (dp) {
-        case 32: return cfg16<32, MFA_D32_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32," MFA_STR(MFA_D32_TILE) ">" : "mfa_fwd16<f16,d32," MFA_STR(MFA_D32_TILE) ">");
-        case 64: return cfg16<64, MFA_D64_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64," MFA_STR(MFA_D64_TILE) ">" : "mfa_fwd16<f16,d64," MFA_STR(MFA_D64_TILE) ">");
-        case 96: return cfg16<96, MFA_D96_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d96," MFA_STR(MFA_D96_TILE) ">" : "mfa_fwd16<f16,d96," MFA_STR(MFA_D96_TILE) ">");
-        default: return cfg16<128, MFA_D128_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d128," MFA_STR(MFA_D128_TILE) ">" : "mfa_fwd16<f16,d128," MFA_STR(MFA_D128_TILE) ">");
+        case 32: return cfg16<32, MFA_D32_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32," MFA_STR(MFA_D32_TILE) ">" : "mfa_fwd16<f16,d32," MFA_STR(MFA_D32_TILE) ">", paged);
+        case 64: return cfg16<64, MFA_D64_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64," MFA_STR(MFA_D64_TILE) ">" : "mfa_fwd16<f16,d64," MFA_STR(MFA_D64_TILE) ">", paged);
+        case 96: return cfg16<96, MFA_D96_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d96," MFA_STR(MFA_D96_TILE) ">" : "mfa_fwd16<f16,d96," MFA_STR(MFA_D96_TILE) ">", paged);
+        default: return cfg16<128, MFA_D128_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d128," MFA_STR(MFA_D128_TILE) ">" : "mfa_fwd16<f16,d128," MFA_STR(MFA_D128_TILE) ">", paged);
     }
 }
 template <bool BIAS>
-KernelCfg select32(int dp) {
+KernelCfg select32(int dp, bool paged) {
     switch (dp) {
-        case 32: return cfg32<32, 1, BIAS>("mfa_fwd32<f32,d32,q32,k32>");
-        case 64: return cfg32<64, 1, BIAS>("mfa_fwd32<f32,d64,q32,k32>");
-        case 96: return cfg32<96, 1, BIAS>("mfa_fwd32<f32,d96,q32,k32>");
-        default: return cfg32<128, 1, BIAS>("mfa_fwd32<f32,d128,q32,k32>");
+        case 32: return cfg32<32, 1, BIAS>("mfa_fwd32<f32,d32,q32,k32>", paged);
+        case 64: return cfg32<64, 1, BIAS>("mfa_fwd32<f32,d64,q32,k32>", paged);
+        case 96: return cfg32<96, 1, BIAS>("mfa_fwd32<f32,d96,q32,k32>", paged);
+        default: return cfg32<128, 1, BIAS>("mfa_fwd32<f32,d128,q32,k32>", paged);
     }
 }
 
@@ -1661,6 +1732,21 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
         return set_err(MFA_ERR_INVALID, "mfa_fwd: window bounds must be >= -1");
     if ((p->cu_seqlens_q == nullptr) != (p->cu_seqlens_k == nullptr))
         return set_err(MFA_ERR_INVALID, "mfa_fwd: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
+    if (p->block_table) {
+        // every key block lies inside one page: block sizes (32..128 keys) and
+        // split chunks divide the page size
+        if (p->page_block_size <= 0 || p->page_block_size % 256 != 0)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd: page_block_size %d must be a positive multiple of 256",
+                           p->page_block_size);
+        if (p->num_pages <= 0) return set_err(MFA_ERR_INVALID, "mfa_fwd: num_pages must be > 0 with a block_table");
+        if (p->block_table_batch_stride < 0)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd: block_table_batch_stride must be >= 0");
+        if (split_keys % 256 != 0)
+            return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: split_keys %d must be a multiple of 256 with a block_table",
+                           split_keys);
+    }
+    if (p->softmax_lse && (p->lse_batch_stride < 0 || p->lse_head_stride < 0))
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: lse strides must be >= 0");
 
     plan->empty = (p->batch == 0 || p->seqlen_q == 0);
     const int es = din == MFA_DTYPE_F32 ? 4 : 2;
@@ -1715,12 +1801,18 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
             return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd_splitkv: split-KV uses the 256-row tiles");
         fills_chip = false;
     }
+    const bool paged = p->block_table != nullptr;
+    if (paged) {
+        if (p->tile_hint == MFA_TILE_PINGPONG)
+            return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles do not take a block_table");
+        fills_chip = false;
+    }
     if (din == MFA_DTYPE_F32)
-        plan->cfg = bias ? select32<true>(dp) : select32<false>(dp);
+        plan->cfg = bias ? select32<true>(dp, paged) : select32<false>(dp, paged);
     else if (din == MFA_DTYPE_BF16)
-        plan->cfg = bias ? select16<true, true>(dp, fills_chip) : select16<true, false>(dp, fills_chip);
+        plan->cfg = bias ? select16<true, true>(dp, fills_chip, paged) : select16<true, false>(dp, fills_chip, paged);
     else
-        plan->cfg = bias ? select16<false, true>(dp, fills_chip) : select16<false, false>(dp, fills_chip);
+        plan->cfg = bias ? select16<false, true>(dp, fills_chip, paged) : select16<false, false>(dp, fills_chip, paged);
 
     KArgs& a = plan->args;
     memset(&a, 0, sizeof(a));
@@ -1748,6 +1840,30 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     a.wr = p->window_right < 0 ? -1 : (int32_t)(p->window_right > wmax ? wmax : p->window_right);
     a.causal = p->causal ? 1 : 0;
     a.out_f32 = dout == MFA_DTYPE_F32 ? 1 : 0;
+    a.lse = p->softmax_lse;
+    a.lse_b = p->lse_batch_stride;
+    a.lse_h = p->lse_head_stride;
+    if (p->block_table) {
+        // j / page for 0 <= j < 2^31 as umulhi(j, m) >> s (round-up method:
+        // l = ceil(log2 page), m = ceil(2^(31+l) / page) < 2^32, s = l - 1)
+        const uint32_t d = (uint32_t)p->page_block_size;
+        int l = 0;
+        while ((1u << l) < d) ++l;
+        const unsigned __int128 one = 1;
+        a.page_m = (uint32_t)(((one << (31 + l)) + d - 1) / d);
+        a.page_s = l - 1;
+        a.page = p->page_block_size;
+        a.npages = p->num_pages;
+        a.bt = p->block_table;
+        a.bt_b = p->block_table_batch_stride;
+    } else {
+        a.page_m = 0;  // one page: j / page = 0, row = j
+        a.page_s = 0;
+        a.page = 0;
+        a.npages = 1;
+        a.bt = nullptr;
+        a.bt_b = 0;
+    }
 
     const int rows = plan->cfg.rows;
     a.T = (p->seqlen_q + rows - 1) / rows;
@@ -1828,8 +1944,8 @@ int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info) {
     info->rows_per_block = plan.cfg.rows;
     info->keys_per_block = plan.cfg.keys;
     info->lds_bytes = plan.cfg.lds;
-    snprintf(info->kernel_name, sizeof(info->kernel_name), "%s%s", plan.cfg.name,
-             (params->softcap > 0.f || params->alibi_slopes) ? "+bias" : "");
+    snprintf(info->kernel_name, sizeof(info->kernel_name), "%s%s%s", plan.cfg.name,
+             (params->softcap > 0.f || params->alibi_slopes) ? "+bias" : "", params->block_table ? "+paged" : "");
     return MFA_OK;
 }
 

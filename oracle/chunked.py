@@ -48,7 +48,7 @@ def broadcast_alibi(alibi_slopes, B, Hq):
 
 
 def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1, alibi=None,
-                chunk=DEFAULT_CHUNK, rows=None):
+                chunk=DEFAULT_CHUNK, rows=None, return_lse=False):
     """Heads-second q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D] (CPU) -> fp32 [B,Hq,Lq,D].
 
     `alibi` is the broadcast [B*Hq] fp32 slope vector or None.  The result is
@@ -57,6 +57,12 @@ def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_righ
     `rows` (other rows are left as NaN); each chunk is computed exactly as in
     the full run, so the subset equals the corresponding rows of the full
     result.
+
+    return_lse=True also returns the fp32 [B,Hq,Lq] log-sum-exp of the same
+    masked scores the softmax at _kernel.py:1205 normalises,
+    torch.logsumexp(scores, -1) (-inf for a row whose keys are all masked).
+    The reference computes but never returns this normaliser; it is the
+    oracle of the build's softmax_lse output.
     """
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
@@ -71,6 +77,7 @@ def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_righ
         vf = vf.repeat_interleave(rep, dim=1)
     kt = kf.transpose(-1, -2)
     out = torch.full((B, Hq, Lq, D), float("nan"), dtype=torch.float32)
+    lse = torch.full((B, Hq, Lq), float("nan"), dtype=torch.float32)
     chunk = max(1, int(chunk))
     wl, wr = int(window_left), int(window_right)
     windowed = wl >= 0 or wr >= 0
@@ -97,7 +104,9 @@ def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_righ
         probs = torch.softmax(scores, dim=-1)
         probs = torch.nan_to_num(probs, nan=0.0)
         out[:, :, start:end] = probs @ vf
-    return out
+        if return_lse:
+            lse[:, :, start:end] = torch.logsumexp(scores, dim=-1)
+    return (out, lse) if return_lse else out
 
 
 def cast_like(out_f32, dtype):
@@ -106,28 +115,35 @@ def cast_like(out_f32, dtype):
 
 
 def flash_attn_func(q, k, v, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
-                    alibi_slopes=None, chunk=DEFAULT_CHUNK, rows=None):
-    """Heads-third q [B,Lq,Hq,D], k/v [B,Lk,Hkv,D] -> fp32 [B,Lq,Hq,D] (__init__.py:62-99)."""
+                    alibi_slopes=None, chunk=DEFAULT_CHUNK, rows=None, return_lse=False):
+    """Heads-third q [B,Lq,Hq,D], k/v [B,Lk,Hkv,D] -> fp32 [B,Lq,Hq,D] (__init__.py:62-99).
+
+    return_lse=True: (out, lse [B,Hq,Lq]) -- see flash_torch.
+    """
     B, _, Hq, D = q.shape
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
     alibi = broadcast_alibi(alibi_slopes, B, Hq) if alibi_slopes is not None else None
-    out = flash_torch(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale, causal, softcap,
-                      window_size[0], window_size[1], alibi, chunk=chunk, rows=rows)
-    return out.transpose(1, 2).contiguous()
+    res = flash_torch(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale, causal, softcap,
+                      window_size[0], window_size[1], alibi, chunk=chunk, rows=rows, return_lse=return_lse)
+    if return_lse:
+        return res[0].transpose(1, 2).contiguous(), res[1]
+    return res.transpose(1, 2).contiguous()
 
 
 def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, causal=False,
-                           window_size=(-1, -1), softcap=0.0, alibi_slopes=None, chunk=DEFAULT_CHUNK):
+                           window_size=(-1, -1), softcap=0.0, alibi_slopes=None, chunk=DEFAULT_CHUNK,
+                           return_lse=False):
     """Packed q [Tq,Hq,D], k/v [Tk,Hkv,D] -> fp32 [Tq,Hq,D] (__init__.py:102-183).
 
     Rows of empty query sequences do not exist; rows of sequences with no
-    keys are 0.
+    keys are 0 (lse -inf).  return_lse=True: (out, lse [Hq, Tq]).
     """
     cu_q = [int(x) for x in torch.as_tensor(cu_seqlens_q).tolist()]
     cu_k = [int(x) for x in torch.as_tensor(cu_seqlens_k).tolist()]
     Hq, D = q.shape[1], q.shape[2]
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
     out = torch.zeros(q.shape, dtype=torch.float32)
+    lse = torch.full((Hq, q.shape[0]), float("-inf"), dtype=torch.float32)
     for i in range(len(cu_q) - 1):
         qs = q[cu_q[i]:cu_q[i + 1]]
         ks = k[cu_k[i]:cu_k[i + 1]]
@@ -138,10 +154,38 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=No
         if alibi_slopes is not None and alibi_slopes.dim() == 2:
             seq_alibi = alibi_slopes[i]
         alibi = broadcast_alibi(seq_alibi, 1, Hq) if seq_alibi is not None else None
-        o = flash_torch(qs.permute(1, 0, 2)[None], ks.permute(1, 0, 2)[None], vs.permute(1, 0, 2)[None],
-                        scale, causal, softcap, window_size[0], window_size[1], alibi, chunk=chunk)
+        if ks.shape[0] == 0:
+            continue  # no keys: zero rows (lse stays -inf)
+        o, l = flash_torch(qs.permute(1, 0, 2)[None], ks.permute(1, 0, 2)[None], vs.permute(1, 0, 2)[None],
+                           scale, causal, softcap, window_size[0], window_size[1], alibi, chunk=chunk,
+                           return_lse=True)
         out[cu_q[i]:cu_q[i + 1]] = o[0].permute(1, 0, 2)
-    return out
+        lse[:, cu_q[i]:cu_q[i + 1]] = l[0]
+    return (out, lse) if return_lse else out
+
+
+def gather_pages(k_pages, block_table, seqlens_k):
+    """Paged K (or V) -> packed [sum(seqlens_k), H, D] (CPU).
+
+    k_pages: [num_pages, page_block_size, H, D]; key j of sequence b is row
+    j % page_block_size of page block_table[b, j // page_block_size] -- the
+    block_table convention of CUDA flash-attn 2.x's flash_attn_varlen_func
+    (the API the reference mirrors and whose version its shim reports, 2.7.4,
+    metal_flash_attn/_version.py:6; flash-attn itself is not a dependency and
+    is absent here), which the reference rejects
+    (metal_flash_attn/__init__.py:130-131).  With this gather, the paged call
+    equals flash_attn_varlen_func on the packed K/V.
+    """
+    kp = k_pages.detach().cpu()
+    bt = torch.as_tensor(block_table).cpu().long()
+    page = kp.shape[1]
+    parts = []
+    for b, n in enumerate(int(x) for x in seqlens_k):
+        j = torch.arange(n)
+        parts.append(kp[bt[b, j // page], j % page])
+    if not parts:
+        return kp.new_zeros((0,) + tuple(kp.shape[2:]))
+    return torch.cat(parts, dim=0)
 
 
 def uneven_v_attention(query, key, value, attn_mask=None, is_causal=False, scale=None, enable_gqa=False,

@@ -16,7 +16,10 @@
  * softmax and its chunked torch path, so that it can pin them.
  *
  * Layout: heads-second, contiguous: q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D],
- * o [B,Hq,Lq,D] (double).  alibi: [B*Hq] or NULL.
+ * o [B,Hq,Lq,D] (double).  alibi: [B*Hq] or NULL.  lse: [B,Hq,Lq] (double)
+ * or NULL; when given, it receives m + log(l), the log of the softmax
+ * normaliser (-inf for a row with no valid key), which the reference
+ * computes but never returns.
  */
 #include <math.h>
 #include <stdlib.h>
@@ -24,7 +27,7 @@
 int oracle_stream_fwd(const float* q, const float* k, const float* v, double* o,
                       int B, int Hq, int Hkv, int Lq, int Lk, int D,
                       int causal, double scale, double softcap, int wl, int wr,
-                      const float* alibi)
+                      const float* alibi, double* lse)
 {
     if (Hkv <= 0 || Hq % Hkv != 0) return -1;
     double* s = (double*)malloc(sizeof(double) * (Lk > 0 ? Lk : 1));
@@ -46,6 +49,7 @@ int oracle_stream_fwd(const float* q, const float* k, const float* v, double* o,
                 long kmin = 0;
                 if (wl >= 0 && center - wl > 0) kmin = center - wl;
                 for (int d = 0; d < D; ++d) oi[d] = 0.0;
+                if (lse) lse[(size_t)(b * Hq + h) * Lq + i] = -INFINITY;
                 if (kmin >= kmax) continue;
                 double m = -INFINITY;
                 for (long j = kmin; j < kmax; ++j) {
@@ -66,6 +70,7 @@ int oracle_stream_fwd(const float* q, const float* k, const float* v, double* o,
                     for (int d = 0; d < D; ++d) oi[d] += p * (double)vj[d];
                 }
                 for (int d = 0; d < D; ++d) oi[d] /= l;
+                if (lse) lse[(size_t)(b * Hq + h) * Lq + i] = m + log(l);
             }
         }
     free(s);

@@ -92,7 +92,17 @@ def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
     (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "head_dim", 128),
                 setattr(p, "q_head_stride", 128)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
     (lambda p: setattr(p, "k_seq_stride", -64), _hip.MFA_ERR_INVALID, "sequence strides"),
+    (lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 256), setattr(p, "num_pages", 4),
+                setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG)), _hip.MFA_ERR_UNSUPPORTED, "block_table"),
     (lambda p: setattr(p, "seqlen_k", -1), _hip.MFA_ERR_INVALID, "negative"),
+    (lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 100), setattr(p, "num_pages", 4)),
+     _hip.MFA_ERR_INVALID, "page_block_size"),
+    (lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 256)), _hip.MFA_ERR_INVALID,
+     "num_pages"),
+    (lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 512), setattr(p, "num_pages", 4),
+                setattr(p, "block_table_batch_stride", -1)), _hip.MFA_ERR_INVALID, "block_table_batch_stride"),
+    (lambda p: (setattr(p, "softmax_lse", 256), setattr(p, "lse_head_stride", -1)), _hip.MFA_ERR_INVALID,
+     "lse strides"),
 ])
 def test_invalid_requests_are_rejected_before_launch(lib, mutate, code, msg):
     p = good_params()
@@ -212,6 +222,8 @@ def test_split_kv_workspace_size(lib):
      _hip.MFA_ERR_UNSUPPORTED, "fp32"),
     (1024, lambda p: setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), _hip.MFA_ERR_UNSUPPORTED, "256-row"),
     (64, lambda p: setattr(p, "seqlen_k", 64 * 1025), _hip.MFA_ERR_INVALID, "exceed"),
+    (192, lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 256), setattr(p, "num_pages", 16)),
+     _hip.MFA_ERR_INVALID, "multiple of 256 with a block_table"),
 ])
 def test_split_kv_invalid_requests(lib, chunk, mutate, code, msg):
     p = good_params(L=4096)

@@ -149,10 +149,45 @@ class TestVarlenContract:
         with pytest.raises(NotImplementedError):
             mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6, dropout_p=0.5)
 
-    def test_block_table_raises(self, fake_device):
+    def test_block_table_contract(self, fake_device):
+        # the reference raises NotImplementedError for block_table
+        # (metal_flash_attn/__init__.py:130-131); this build implements the paged
+        # layout of CUDA flash-attn and validates it before any launch
         q, k, v, cu_q, cu_k = self.make()
-        with pytest.raises(NotImplementedError):
-            mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6, block_table=torch.zeros(1, 1, dtype=torch.int32))
+        pool = t(3, 256, 2, 32)
+        bt = torch.tensor([[0], [2]], dtype=torch.int32)
+        with pytest.raises(ValueError):  # k/v not page pools
+            mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6, block_table=bt)
+        with pytest.raises(ValueError):  # page size not a multiple of 256
+            mfa.flash_attn_varlen_func(q, t(3, 100, 2, 32), t(3, 100, 2, 32), cu_q, cu_k, 7, 6, block_table=bt)
+        with pytest.raises(ValueError):  # int64 table
+            mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6, block_table=bt.long())
+        with pytest.raises(ValueError):  # one row per sequence
+            mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6, block_table=bt[:1])
+        with pytest.raises(ValueError):  # page id outside the pool
+            mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6,
+                                       block_table=torch.tensor([[0], [3]], dtype=torch.int32))
+        with pytest.raises(ValueError):  # too few pages for 300 keys
+            mfa.flash_attn_varlen_func(q, pool, pool, cu_q, torch.tensor([0, 300, 303], dtype=torch.int32),
+                                       7, 300, block_table=bt)
+        assert not fake_device
+        # unused entries (past a sequence's last page) are never checked or read
+        out = mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6,
+                                         block_table=torch.tensor([[1, -5], [2, 99]], dtype=torch.int32))
+        call = fake_device[-1]
+        assert out.shape == q.shape and call["k"].shape == pool.shape and call["block_table"] is not None
+        assert call["seqlen_k"] == 6 and call["lse"] is None
+
+    def test_with_lse_layouts(self, fake_device):
+        q, k, v, cu_q, cu_k = self.make()
+        out, lse = mfa.flash_attn_varlen_func_with_lse(q, k, v, cu_q, cu_k, 7, 6, causal=True)
+        assert out.shape == q.shape and lse.shape == (4, 12) and lse.dtype == torch.float32
+        assert fake_device[-1]["lse"] is lse
+        qd, kd, vd = t(2, 9, 4, 32), t(2, 5, 2, 32), t(2, 5, 2, 32)
+        out, lse = mfa.flash_attn_func_with_lse(qd, kd, vd)
+        assert out.shape == qd.shape and lse.shape == (2, 4, 9) and lse.dtype == torch.float32
+        with pytest.raises(ValueError):
+            mfa.flash_attn_func_with_lse(qd, kd, vd, softcap=-1.0)
 
     def test_shape_errors(self, fake_device):
         q, k, v, cu_q, cu_k = self.make()

@@ -339,3 +339,79 @@ def test_uneven_v_single_key_and_gqa():
     assert torch.allclose(out, v.repeat_interleave(2, dim=1).expand(1, 4, 5, 40), atol=0)
     with pytest.raises(ValueError):
         chunked.uneven_v_attention(q, k, v)  # Hq != Hkv without enable_gqa
+
+
+# --------------------------------------------------------------------------- softmax_lse, merge, paging
+# The reference computes the softmax normaliser but never returns it; the
+# oracle's lse (torch.logsumexp of the masked scores) is pinned against the
+# float64 C statement's m + log(l) and against closed forms.
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(i) for i in range(len(CASES))])
+@pytest.mark.parametrize("shape", [(2, 4, 2, 33, 33, 16), (1, 4, 1, 45, 20, 24)], ids=["square-gqa", "lq>lk-mqa"])
+def test_lse_matches_float64_stream(case, shape):
+    B, Hq, Hkv, Lq, Lk, D = shape
+    q, k, v = qkv(B, Hq, Hkv, Lq, Lk, D, seed=15)
+    kw = dict(case)
+    al = kw.pop("alibi", None)
+    alibi = None
+    if al is not None:
+        alibi = chunked.broadcast_alibi(torch.linspace(0.05, 0.6, Hq).repeat(B, 1), B, Hq)
+    out, lse = chunked.flash_torch(q, k, v, 0.3, alibi=alibi, return_lse=True, **kw)
+    ref_out, ref_lse = stream.stream_fwd(q, k, v, 0.3, alibi=alibi, return_lse=True, **kw)
+    assert torch.equal(torch.isinf(lse), torch.isinf(ref_lse))
+    fin = torch.isfinite(ref_lse)
+    close(lse[fin], ref_lse[fin])
+    close(out, ref_out)
+
+
+def test_lse_zero_query_is_log_of_the_valid_key_count():
+    # q = 0: every valid score is 0, so lse = ln(number of valid keys)
+    _, k, v = qkv(1, 2, 2, 5, 9, 8, seed=16)
+    q = torch.zeros(1, 2, 5, 8)
+    _, lse = chunked.flash_torch(q, k, v, 0.5, True, return_lse=True)
+    counts = torch.arange(5) + 1 + (9 - 5)  # bottom-right causal: keys 0..i+4
+    close(lse, torch.log(counts.double()).expand(1, 2, 5))
+    _, lse = chunked.flash_torch(q, k, v, 0.5, True, window_left=2, return_lse=True)
+    close(lse, torch.full((1, 2, 5), math.log(3.0)))
+
+
+def test_lse_single_key_is_its_transformed_score():
+    q, k, v = qkv(1, 1, 1, 4, 1, 16, seed=17)
+    _, lse = chunked.flash_torch(q, k, v, 0.7, False, softcap=3.0, return_lse=True)
+    s = 3.0 * torch.tanh((q[0, 0] @ k[0, 0].T).squeeze(-1) * 0.7 / 3.0)
+    close(lse[0, 0], s)
+
+
+def test_lse_of_rows_without_keys_is_minus_inf():
+    q, k, v = qkv(1, 2, 2, 7, 3, 8, seed=18)
+    out, lse = chunked.flash_torch(q, k, v, 0.5, True, return_lse=True)
+    assert torch.isneginf(lse[:, :, :4]).all() and torch.isfinite(lse[:, :, 4:]).all()
+    assert (out[:, :, :4] == 0).all()
+    _, vl = chunked.flash_attn_varlen_func(torch.randn(3, 2, 8), torch.randn(0, 2, 8), torch.randn(0, 2, 8),
+                                           torch.tensor([0, 3]), torch.tensor([0, 0]), return_lse=True)
+    assert torch.isneginf(vl).all()
+
+
+@pytest.mark.parametrize("softcap", [0.0, 2.0])
+def test_merge_of_key_shards_equals_full_attention(softcap):
+    import mtlflashattn_amd as mfa
+
+    q, k, v = qkv(2, 4, 2, 6, 40, 16, seed=19)
+    full, full_lse = chunked.flash_torch(q, k, v, 0.4, False, softcap=softcap, return_lse=True)
+    parts = [chunked.flash_torch(q, k[:, :, a:b], v[:, :, a:b], 0.4, False, softcap=softcap, return_lse=True)
+             for a, b in ((0, 13), (13, 14), (14, 40), (40, 40))]  # the last shard is empty
+    # flash_torch is heads-second; the merge takes the heads-third output layout
+    out, lse = mfa.merge_attention_partials([o.transpose(1, 2) for o, _ in parts], [l for _, l in parts])
+    close(out.transpose(1, 2), full)
+    close(lse, full_lse)
+    out, lse = mfa.merge_attention_partials([parts[3][0].transpose(1, 2)], [parts[3][1]])
+    assert (out == 0).all() and torch.isneginf(lse).all()
+
+
+def test_gather_pages_follows_the_block_table():
+    pool = (100 * torch.arange(4)[:, None] + torch.arange(4)[None, :]).float()[:, :, None, None].expand(4, 4, 1, 2)
+    table = torch.tensor([[2, 0], [-1, -1], [1, 3]], dtype=torch.int32)  # row 1 has no keys: never read
+    got = chunked.gather_pages(pool, table, [5, 0, 8])
+    want = torch.tensor([200, 201, 202, 203, 0, 100, 101, 102, 103, 300, 301, 302, 303]).float()
+    assert torch.equal(got[:, 0, 0], want) and torch.equal(got[:, 0, 1], want)
