@@ -183,6 +183,37 @@ def cpu_baseline(cfg: int, budget_s: float = 12.0):
             "note": "formula FLOPs of the sample (4*H*Lq*Lk*D, halved for causal) / median of 3 runs"}
 
 
+def make_backward_step(c):
+    """A closure running the HIP backward (dq, dk, dv) of config c's forward:
+    out / lse / dout prepared once, outside the timed region."""
+    import math
+
+    import torch
+
+    from mtlflashattn_amd import _kernel
+
+    kw = c["kw"]
+    scale = 1.0 / math.sqrt(c["D"])
+    wl, wr = kw.get("window_size", (-1, -1))
+    cfgk = dict(scale=scale, causal=kw.get("causal", False), softcap=kw.get("softcap", 0.0), window_left=wl,
+                window_right=wr)
+    g = torch.Generator().manual_seed(99)
+    if c["varlen"] is not None:
+        cu, mx = c["varlen"]
+        out, lse = _kernel.forward_varlen(c["q"], c["k"], c["v"], cu, cu, mx, mx, return_lse=True, **cfgk)
+        dout = torch.randn(out.shape, generator=g).to(out.device, out.dtype)
+        q, k, v, o, d = (t[None] for t in (c["q"], c["k"], c["v"], out, dout))
+        extra = dict(cu_q=cu, cu_k=cu, seqlen_q=mx, seqlen_k=mx)
+    else:
+        out, lse = _kernel.forward_bshd(c["q"], c["k"], c["v"], alibi_slopes=kw.get("alibi_slopes"),
+                                        return_lse=True, **cfgk)
+        dout = torch.randn(out.shape, generator=g).to(out.device, out.dtype)
+        q, k, v, o, d = c["q"], c["k"], c["v"], out, dout
+        extra = {}
+    alibi, bstride = _kernel._alibi_arg(kw.get("alibi_slopes"), q.shape[0], q.shape[2], q.device)
+    return lambda: _kernel._run_bwd(q, k, v, o, d, lse, alibi=alibi, alibi_bstride=bstride, **cfgk, **extra)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,6 +223,9 @@ def main():
                     help="BASELINE config 2-5 (default 2, the headline); 6-8 are HBM-bound short-L "
                          "shapes (roofline in GB/s; 8 runs split-KV)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--backward", action="store_true",
+                    help="time the HIP backward (dq, dk, dv) of the config instead of the forward (configs 2-5; "
+                         "effective TFLOP/s = 10*D FLOPs per valid pair; no CPU baseline)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, run one plain 256 MiB device copy (rocprofv3 PMC calibration of "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -207,8 +241,15 @@ def main():
     from mtlflashattn_amd import _kernel
 
     c = make_config(args.config)
+    step = (lambda: run_step(c))
+    if args.backward:
+        if args.config not in (2, 3, 4, 5):
+            raise SystemExit("--backward takes configs 2-5")
+        step = make_backward_step(c)
+        c = dict(c, formula=c["formula"] * 5 // 2, algo=c["algo"] * 5 // 2)
+        args.no_cpu_baseline = True
     for _ in range(args.warmup):
-        run_step(c)
+        step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     # whole-job timing: K back-to-back steps
@@ -216,7 +257,7 @@ def main():
     t_end = torch.cuda.Event(enable_timing=True)
     t_start.record(stream)
     for _ in range(args.steps):
-        run_step(c)
+        step()
     t_end.record(stream)
     torch.cuda.synchronize()
     ms_total = t_start.elapsed_time(t_end)
@@ -225,7 +266,7 @@ def main():
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     for a, b in evs:
         a.record(stream)
-        run_step(c)
+        step()
         b.record(stream)
     torch.cuda.synchronize()
     kernel_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
@@ -233,7 +274,9 @@ def main():
     value = c["formula"] / (ms_step / 1e3) / 1e12
     peak = PEAK_TFLOPS[c["dtype"]]
     achieved = c["algo"] / (kernel_ms / 1e3) / 1e12
-    if c["varlen"] is not None:
+    if args.backward:
+        kname = "mfa_bwd_dsum + mfa_bwd_dkdv + mfa_bwd_dq"
+    elif c["varlen"] is not None:
         info = None
         kname = "mfa_fwd16 (varlen)"
     else:
@@ -246,9 +289,9 @@ def main():
         chunk = _kernel.split_chunk(c["q"], c["k"])
         if chunk:
             kname += f" split-KV {chunk} keys + mfa_combine"
-    traffic = measured_traffic(args.config)
+    traffic = None if args.backward else measured_traffic(args.config)
     line = {
-        "metric": METRIC,
+        "metric": METRIC if not args.backward else "attn bwd effective TFLOP/s (10*D FLOPs per valid pair)",
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MFA_ABI_VERSION 3
+#define MFA_ABI_VERSION 4
 
 /* element types (dtype_in / dtype_out) */
 #define MFA_DTYPE_F16 0
@@ -210,6 +210,48 @@ int32_t mfa_fwd_split_keys(const mfa_fwd_params* params);
 int64_t mfa_fwd_workspace_bytes(const mfa_fwd_params* params, int32_t split_keys);
 int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* workspace, int64_t workspace_bytes,
                     void* stream);
+
+/*
+ * Backward pass (gradients of q, k, v).  No counterpart in the reference,
+ * which is forward-only (metal_flash_attn/__init__.py:3-4, README.md:159-161;
+ * training callers fall back to other attention).  Same masking and bias
+ * semantics as the forward; the forward's O and softmax_lse are inputs:
+ *   P = exp(s - lse), dV = P^T dO, dP = dO V^T, Dsum = rowsum(dO * O),
+ *   dS = P * (dP - Dsum) [* (1 - tanh^2) under softcap], dQ = scale dS K,
+ *   dK = scale dS^T Q.
+ * With grouped-query heads, dK/dV of a K/V head sum over its query heads.
+ * Deterministic (no atomics): one kernel owns each dK/dV block and loops over
+ * every query of its K/V head; another owns each dQ block.
+ */
+typedef struct mfa_bwd_params {
+    /* q, k, v, o (the forward output), shapes, strides, masks and biases as
+     * in the forward; fwd.softmax_lse (+ strides) is the forward's lse and
+     * required; fwd.block_table must be NULL; fwd.tile_hint is ignored;
+     * fwd.dtype_out is o's dtype (dtype_in or fp32). */
+    mfa_fwd_params fwd;
+    const void* dout; /* dL/dO, laid out like o (its own strides), o's dtype */
+    int64_t do_batch_stride, do_seq_stride, do_head_stride;
+    void* dq;         /* laid out like q */
+    int64_t dq_batch_stride, dq_seq_stride, dq_head_stride;
+    void* dk;         /* laid out like k */
+    int64_t dk_batch_stride, dk_seq_stride, dk_head_stride;
+    void* dv;         /* laid out like v */
+    int64_t dv_batch_stride, dv_seq_stride, dv_head_stride;
+    int32_t dtype_grad; /* dtype of dq/dk/dv: dtype_in or MFA_DTYPE_F32 */
+    int32_t reserved;
+} mfa_bwd_params;
+
+/* 1 if mfa_bwd implements (dtype_in, head_dim): bf16/fp16, head_dim a
+ * multiple of 8 up to MFA_MAX_HEAD_DIM. */
+int mfa_bwd_supported(int32_t dtype_in, int32_t head_dim);
+/* Device workspace mfa_bwd needs (the fp32 row sums Dsum), 0 for an empty
+ * problem, < 0 on error. */
+int64_t mfa_bwd_workspace_bytes(const mfa_bwd_params* params);
+/* Enqueue the backward kernels on `stream`; `workspace`: 256-byte aligned
+ * device buffer of at least mfa_bwd_workspace_bytes bytes, owned by the
+ * caller.  Never synchronizes, never allocates. */
+int mfa_bwd(const mfa_bwd_params* params, void* workspace, int64_t workspace_bytes, void* stream);
+int mfa_bwd_params_size(void);
 
 #ifdef __cplusplus
 }

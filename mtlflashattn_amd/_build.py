@@ -16,7 +16,7 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-SRC = os.path.join(PKG_DIR, "csrc", "mfa_fwd.hip")
+SRCS = [os.path.join(PKG_DIR, "csrc", name) for name in ("mfa_fwd.hip", "mfa_bwd.hip")]
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libmtlfa_hip.so"
@@ -46,7 +46,7 @@ def build(verbose: bool = False) -> str:
     """Compile the kernel library; returns its path.  Always recompiles."""
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE}", SRC, "-o", tmp]
+    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE}", *SRCS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -21,7 +21,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime first)
 
 from ._build import LIB_PATH
 
-MFA_ABI_VERSION = 3
+MFA_ABI_VERSION = 4
 MFA_DTYPE_F16 = 0
 MFA_DTYPE_BF16 = 1
 MFA_DTYPE_F32 = 2
@@ -63,6 +63,19 @@ class MfaFwdParams(ctypes.Structure):
         ("softmax_lse", _c_ptr), ("lse_batch_stride", _c_i64), ("lse_head_stride", _c_i64),
         ("block_table", _c_ptr), ("block_table_batch_stride", _c_i64),
         ("page_block_size", _c_i32), ("num_pages", _c_i32),
+    ]
+
+
+class MfaBwdParams(ctypes.Structure):
+    """Mirror of `mfa_bwd_params` (include/mfa.h)."""
+
+    _fields_ = [
+        ("fwd", MfaFwdParams),
+        ("dout", _c_ptr), ("do_batch_stride", _c_i64), ("do_seq_stride", _c_i64), ("do_head_stride", _c_i64),
+        ("dq", _c_ptr), ("dq_batch_stride", _c_i64), ("dq_seq_stride", _c_i64), ("dq_head_stride", _c_i64),
+        ("dk", _c_ptr), ("dk_batch_stride", _c_i64), ("dk_seq_stride", _c_i64), ("dk_head_stride", _c_i64),
+        ("dv", _c_ptr), ("dv_batch_stride", _c_i64), ("dv_seq_stride", _c_i64), ("dv_head_stride", _c_i64),
+        ("dtype_grad", _c_i32), ("reserved", _c_i32),
     ]
 
 
@@ -124,9 +137,22 @@ def load():
         lib.mfa_fwd_workspace_bytes.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32]
         lib.mfa_fwd_splitkv.restype = ctypes.c_int
         lib.mfa_fwd_splitkv.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32, _c_ptr, ctypes.c_int64, _c_ptr]
+        lib.mfa_bwd_params_size.restype = ctypes.c_int
+        lib.mfa_bwd_params_size.argtypes = []
+        lib.mfa_bwd_supported.restype = ctypes.c_int
+        lib.mfa_bwd_supported.argtypes = [_c_i32, _c_i32]
+        lib.mfa_bwd_workspace_bytes.restype = ctypes.c_int64
+        lib.mfa_bwd_workspace_bytes.argtypes = [ctypes.POINTER(MfaBwdParams)]
+        lib.mfa_bwd.restype = ctypes.c_int
+        lib.mfa_bwd.argtypes = [ctypes.POINTER(MfaBwdParams), _c_ptr, ctypes.c_int64, _c_ptr]
         if lib.mfa_abi_version() != MFA_ABI_VERSION:
             raise HipLibraryError(
                 f"mtlflashattn_amd: {path} has ABI {lib.mfa_abi_version()}, expected {MFA_ABI_VERSION}; rebuild it"
+            )
+        if lib.mfa_bwd_params_size() != ctypes.sizeof(MfaBwdParams):
+            raise HipLibraryError(
+                f"mtlflashattn_amd: mfa_bwd_params is {lib.mfa_bwd_params_size()} bytes in {path} but "
+                f"{ctypes.sizeof(MfaBwdParams)} in the ctypes mirror; rebuild it"
             )
         if lib.mfa_params_size() != ctypes.sizeof(MfaFwdParams):
             raise HipLibraryError(
@@ -176,6 +202,21 @@ def fwd_splitkv(params: MfaFwdParams, chunk: int, workspace: int, workspace_byte
                              _c_ptr(stream))
     if rc != MFA_OK:
         raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_fwd_splitkv failed ({rc})")
+
+
+def bwd_workspace_bytes(params: MfaBwdParams) -> int:
+    lib = load()
+    n = lib.mfa_bwd_workspace_bytes(ctypes.byref(params))
+    if n < 0:
+        raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_bwd_workspace_bytes failed ({n})")
+    return int(n)
+
+
+def bwd(params: MfaBwdParams, workspace: int, workspace_bytes_: int, stream: int) -> None:
+    lib = load()
+    rc = lib.mfa_bwd(ctypes.byref(params), _c_ptr(workspace), int(workspace_bytes_), _c_ptr(stream))
+    if rc != MFA_OK:
+        raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_bwd failed ({rc})")
 
 
 def launch_info(params: MfaFwdParams) -> MfaLaunchInfo:

@@ -367,6 +367,12 @@ def flash_attn_forward(q, k, v, scale, causal, softcap=0.0, window_left=-1, wind
         raise NotImplementedError(f"mtlflashattn_amd: dtype {q.dtype} (q/k/v must match, fp16/bf16/fp32)")
     if D > MAX_HEAD_DIM:
         raise NotImplementedError(f"mtlflashattn_amd: head_dim {D} > {MAX_HEAD_DIM}")
+    if _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
+        # differentiable path (heads-third views of the same tensors)
+        o, lse = _FlashAttnFn.apply(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale, causal,
+                                    softcap, window_left, window_right, alibi_slopes)
+        o = o.transpose(1, 2).contiguous()
+        return (o, lse) if return_lse else o
     out = torch.empty(B, Hq, Lq, D, dtype=_out_dtype(q, out_dtype), device=q.device)
     lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device) if return_lse else None
     _run(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2),
@@ -389,6 +395,10 @@ def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_rig
     if softcap < 0:
         raise ValueError("mtlflashattn_amd: softcap must be >= 0 (0 disables capping)")
     B, Lq, Hq, D = q.shape
+    if _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
+        _alibi_arg(alibi_slopes, B, Hq, q.device)  # validate before autograd records anything
+        o, lse = _FlashAttnFn.apply(q, k, v, scale, causal, softcap, window_left, window_right, alibi_slopes)
+        return (o, lse) if return_lse else o
     alibi, bstride = _alibi_arg(alibi_slopes, B, Hq, q.device)
     out = torch.empty(B, Lq, Hq, D, dtype=_out_dtype(q, out_dtype), device=q.device)
     lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device) if return_lse else None
@@ -398,7 +408,8 @@ def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_rig
 
 
 def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0, window_left=-1,
-                   window_right=-1, alibi_slopes=None, out_dtype=None, return_lse=False, block_table=None):
+                   window_right=-1, alibi_slopes=None, out_dtype=None, return_lse=False, block_table=None,
+                   _grad=True):
     """Packed varlen forward in ONE launch: q [Tq,Hq,D], k/v [Tk,Hkv,D].
 
     cu_q/cu_k: int32 [batch+1] device tensors; max_q/max_k: the longest
@@ -406,7 +417,9 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
     dispatches (metal_flash_attn/__init__.py:165-182) with the same result.
     return_lse=True returns (out, lse [Hq, Tq] fp32).  block_table: int32
     [batch, pages per sequence]; k/v are then a page pool
-    [num_pages, page_block_size, Hkv, D] and cu_k gives the key counts only.
+    [num_pages, page_block_size, Hkv, D] and cu_k gives the key counts only
+    (paged calls are forward-only).  Inputs that require grad (and no block
+    table, q.dtype output) go through the HIP backward.
     """
     batch = cu_q.shape[0] - 1
     Hq = q.shape[1]
@@ -416,8 +429,12 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
             f"got {tuple(alibi_slopes.shape)}"
         )
     alibi, bstride = _alibi_arg(alibi_slopes, batch, Hq, q.device)
-    if _trace_enabled():
+    if _trace_enabled() and _grad:
         _record_trace(q.dtype, q.shape[-1], max_q, max_k, causal, "hip-varlen")
+    if _grad and block_table is None and _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
+        o, lse = _FlashAttnVarlenFn.apply(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left,
+                                          window_right, alibi_slopes)
+        return (o, lse) if return_lse else o
     out = torch.empty(q.shape, dtype=_out_dtype(q, out_dtype), device=q.device)
     lse = torch.empty(Hq, q.shape[0], dtype=torch.float32, device=q.device) if return_lse else None
     cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
@@ -431,6 +448,137 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
          alibi=alibi, alibi_bstride=bstride, cu_q=cu_q, cu_k=cu_k, seqlen_q=max_q, seqlen_k=max_k, lse=lse,
          block_table=block_table)
     return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------
+# backward (the reference is forward-only, metal_flash_attn/__init__.py:3-4;
+# README.md:159-161): HIP kernels behind mfa_bwd, wired into autograd
+
+
+def _needs_grad(*tensors):
+    return torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+
+
+def _run_bwd(q, k, v, out, dout, lse, *, scale, causal, softcap, window_left, window_right, alibi, alibi_bstride,
+             cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None, grad_f32=False):
+    """(dq, dk, dv) of the forward on [B, S, H, D] views (varlen: [1, T, H, D]).
+
+    out: the forward's output in q.dtype; lse: its softmax_lse ([B, Hq, Lq]
+    dense, [Hq, T] varlen).  Returns new tensors shaped like q, k, v in
+    q.dtype (grad_f32=True: fp32, the parity mode).
+    """
+    _kernel_mode()
+    if q.dtype == torch.float32:
+        raise NotImplementedError("mtlflashattn_amd: the backward takes bf16/fp16 inputs (no fp32 HIP backward)")
+    _check_device(q, k, v, out, dout)
+    B, Sq, Hq, D = q.shape
+    Hkv = k.shape[2]
+    varlen = cu_q is not None
+    batch = (cu_q.shape[0] - 1) if varlen else B
+    Lq = int(seqlen_q) if varlen else Sq
+    Lk = int(seqlen_k) if varlen else k.shape[1]
+    gdt = torch.float32 if grad_f32 else q.dtype
+    if batch == 0 or Lq == 0 or Lk == 0 or Hq == 0 or q.numel() == 0 or k.numel() == 0:
+        return tuple(torch.zeros(t.shape, dtype=gdt, device=t.device) for t in (q, k, v))
+    Dp = -(-D // 8) * 8
+    ts = [q, k, v, out, dout.to(q.dtype)]
+    if Dp != D:
+        ts = [F.pad(t, (0, Dp - D)) for t in ts]
+    q_, k_, v_, o_, do_ = (t if _fits_abi(t) else t.contiguous() for t in ts)
+    dq = torch.empty(q_.shape, dtype=gdt, device=q.device)
+    dk = torch.empty(k_.shape, dtype=gdt, device=q.device)
+    dv = torch.empty(v_.shape, dtype=gdt, device=q.device)
+
+    bp = _hip.MfaBwdParams()
+    p = bp.fwd
+    p.q, p.k, p.v, p.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o_.data_ptr()
+    p.q_batch_stride, p.q_seq_stride, p.q_head_stride = _strides_bsh(q_)
+    p.k_batch_stride, p.k_seq_stride, p.k_head_stride = _strides_bsh(k_)
+    p.v_batch_stride, p.v_seq_stride, p.v_head_stride = _strides_bsh(v_)
+    p.o_batch_stride, p.o_seq_stride, p.o_head_stride = _strides_bsh(o_)
+    p.batch, p.heads_q, p.heads_kv = batch, Hq, Hkv
+    p.seqlen_q, p.seqlen_k, p.head_dim = Lq, Lk, Dp
+    if varlen:
+        p.cu_seqlens_q, p.cu_seqlens_k = cu_q.data_ptr(), cu_k.data_ptr()
+    p.scale, p.softcap = float(scale), float(softcap)
+    p.window_left, p.window_right = int(window_left), int(window_right)
+    p.causal = 1 if causal else 0
+    if alibi is not None:
+        p.alibi_slopes = alibi.data_ptr()
+        p.alibi_batch_stride = alibi_bstride
+    p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
+    lse = lse.contiguous()
+    p.softmax_lse = lse.data_ptr()
+    p.lse_batch_stride, p.lse_head_stride = (0, lse.stride(0)) if varlen else (lse.stride(0), lse.stride(1))
+    bp.dout = do_.data_ptr()
+    bp.do_batch_stride, bp.do_seq_stride, bp.do_head_stride = _strides_bsh(do_)
+    bp.dq = dq.data_ptr()
+    bp.dq_batch_stride, bp.dq_seq_stride, bp.dq_head_stride = _strides_bsh(dq)
+    bp.dk = dk.data_ptr()
+    bp.dk_batch_stride, bp.dk_seq_stride, bp.dk_head_stride = _strides_bsh(dk)
+    bp.dv = dv.data_ptr()
+    bp.dv_batch_stride, bp.dv_seq_stride, bp.dv_head_stride = _strides_bsh(dv)
+    bp.dtype_grad = _hip.DTYPE_CODES[gdt]
+    device = q.device
+    with torch.cuda.device(device):
+        nbytes = _hip.bwd_workspace_bytes(bp)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _hip.bwd(bp, ws.data_ptr(), nbytes, torch._C._cuda_getCurrentRawStream(device.index))
+    if Dp != D:
+        dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
+    return dq, dk, dv
+
+
+class _FlashAttnFn(torch.autograd.Function):
+    """Heads-third dense attention with the HIP backward; returns (out, lse),
+    lse not differentiable."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, causal, softcap, window_left, window_right, alibi_slopes):
+        B, Lq, Hq, D = q.shape
+        alibi, bstride = _alibi_arg(alibi_slopes, B, Hq, q.device)
+        out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
+        lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device)
+        _run(q, k, v, out, scale=scale, causal=causal, softcap=softcap, window_left=window_left,
+             window_right=window_right, alibi=alibi, alibi_bstride=bstride, lse=lse)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.cfg = dict(scale=scale, causal=causal, softcap=softcap, window_left=window_left,
+                       window_right=window_right, alibi=alibi, alibi_bstride=bstride)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = _run_bwd(q, k, v, out, dout, lse, **ctx.cfg)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+class _FlashAttnVarlenFn(torch.autograd.Function):
+    """Packed varlen attention with the HIP backward; returns (out, lse [Hq, T])."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left, window_right,
+                alibi_slopes):
+        out, lse = forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left,
+                                  window_right, alibi_slopes, return_lse=True, _grad=False)
+        batch, Hq = cu_q.shape[0] - 1, q.shape[1]
+        alibi, bstride = _alibi_arg(alibi_slopes, batch, Hq, q.device)
+        cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
+        cu_k = cu_k.to(device=q.device, dtype=torch.int32).contiguous()
+        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k)
+        ctx.cfg = dict(scale=scale, causal=causal, softcap=softcap, window_left=window_left,
+                       window_right=window_right, alibi=alibi, alibi_bstride=bstride, seqlen_q=max_q,
+                       seqlen_k=max_k)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse, cu_q, cu_k = ctx.saved_tensors
+        dq, dk, dv = _run_bwd(q[None], k[None], v[None], out[None], dout[None], lse, cu_q=cu_q, cu_k=cu_k,
+                              **ctx.cfg)
+        return dq[0], dk[0], dv[0], None, None, None, None, None, None, None, None, None, None
 
 
 def split_chunk(q, k):

@@ -1,0 +1,715 @@
+// mfa_bwd.hip -- MI355X (gfx950 / CDNA4) flash-attention backward kernels and
+// the mfa_bwd* entry points of include/mfa.h.
+//
+// The reference is forward-only (metal_flash_attn/__init__.py:3-4); these are
+// the gradients of its forward semantics (metal_flash_attn/_kernel.py:32-87:
+// bottom-right causal and sliding-window masks, soft-cap, ALiBi, grouped-query
+// heads, varlen sequences).  With x = scale * q.k, s = cap * tanh(x / cap)
+// (soft-cap) - slope * |center - j| (ALiBi), P = exp(s - lse):
+//   dV = P^T dO,  dP = dO V^T,  Dsum = rowsum(dO * O),
+//   dS = P * (dP - Dsum) * (1 - tanh^2)   (the last factor with soft-cap only),
+//   dQ = scale * dS K,  dK = scale * dS^T Q.
+//
+// Three kernels, no atomics (the result does not depend on scheduling):
+//  * mfa_bwd_dsum_kernel: Dsum per query row (fp32), 16 lanes per row.
+//  * mfa_bwd_dkdv_kernel: a workgroup owns 128 keys of one (sequence, K/V
+//    head), 32 per wavefront, with K and V resident in registers as MFMA B
+//    operands.  It walks every query block (32 rows, staged in LDS with their
+//    dO, lse and Dsum) of every query head of the K/V group that can see its
+//    keys.  S = Q K^T and dP = dO V^T come out with lane = key, so P and dS
+//    feed dV^T += dO^T P and dK^T += Q^T dS straight from the accumulators
+//    (rounded to 16 bits), with dO^T / Q^T read from LDS by
+//    ds_read_b64_tr_b16 -- the same operand scheme as the forward's O^T.
+//  * mfa_bwd_dq_kernel: a workgroup owns 128 query rows, 32 per wavefront,
+//    with Q and dO resident in registers; it walks the key blocks (64 keys,
+//    staged in LDS) its rows can see.  S^T = K Q^T and dP^T = V dO^T give
+//    lane = query, and dQ^T += K^T dS^T takes dS^T from the accumulators.
+// Masks are applied element-wise in every block (the backward is matrix-core
+// bound: four or three GEMMs per tile against a handful of vector ops).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "mfa.h"
+#include "mfa_common.h"
+
+namespace {
+
+constexpr int kBThreads = 256;  // 4 wavefronts
+
+struct BArgs {
+    KArgs f;  // forward arguments: q, k, v, o, strides, shapes, masks, lse (input)
+    const char* dout;
+    int64_t dob, dos, doh;
+    char* dq;
+    int64_t dqb, dqs, dqh;
+    char* dk;
+    int64_t dkb, dks, dkh;
+    char* dv;
+    int64_t dvb, dvs, dvh;
+    float* dsum;       // [B*Hq][Lq] rowsum(dO * O)
+    int32_t grad_f32;  // dq/dk/dv written as fp32
+    int32_t T;         // tiles per unit (dsum: 16-row groups; dK/dV: key tiles; dQ: query tiles)
+    int32_t Ukv;       // (sequence, K/V head) units = B * Hkv
+};
+
+// Per (sequence, query head): q, o, dO, dq, lse and Dsum rows.
+struct QView {
+    const char* q;
+    const char* o;
+    const char* dout;
+    char* dq;
+    const float* lse;
+    float* dsum;
+    int Lq, Lk;
+};
+__device__ __forceinline__ QView q_view(const BArgs& a, int b, int hq) {
+    const KArgs& f = a.f;
+    QView s;
+    int64_t qs = 0, qb = 0;
+    if (f.cu_q) {
+        const int q0 = f.cu_q[b];
+        s.Lq = f.cu_q[b + 1] - q0;
+        s.Lk = f.cu_k[b + 1] - f.cu_k[b];
+        qs = q0;
+        s.lse = f.lse + (int64_t)hq * f.lse_h + q0;
+    } else {
+        s.Lq = f.Lq;
+        s.Lk = f.Lk;
+        qb = b;
+        s.lse = f.lse + (int64_t)b * f.lse_b + (int64_t)hq * f.lse_h;
+    }
+    s.q = f.q + (qb * f.qb + qs * f.qs + (int64_t)hq * f.qh) * 2;
+    s.o = f.o + (qb * f.ob + qs * f.os + (int64_t)hq * f.oh) * 2;
+    s.dout = a.dout + (qb * a.dob + qs * a.dos + (int64_t)hq * a.doh) * 2;
+    const int ges = a.grad_f32 ? 4 : 2;
+    s.dq = a.dq + (qb * a.dqb + qs * a.dqs + (int64_t)hq * a.dqh) * ges;
+    s.dsum = a.dsum + ((int64_t)b * f.Hq + hq) * f.Lq;
+    return s;
+}
+
+// Per (sequence, K/V head): k, v, dk, dv rows.
+struct KView {
+    const char* k;
+    const char* v;
+    char* dk;
+    char* dv;
+    int Lk;
+};
+__device__ __forceinline__ KView k_view(const BArgs& a, int b, int hkv) {
+    const KArgs& f = a.f;
+    KView s;
+    int64_t ks = 0, kb = 0;
+    if (f.cu_k) {
+        ks = f.cu_k[b];
+        s.Lk = f.cu_k[b + 1] - f.cu_k[b];
+    } else {
+        kb = b;
+        s.Lk = f.Lk;
+    }
+    s.k = f.k + (kb * f.kb + ks * f.ks + (int64_t)hkv * f.kh) * 2;
+    s.v = f.v + (kb * f.vb + ks * f.vs + (int64_t)hkv * f.vh) * 2;
+    const int ges = a.grad_f32 ? 4 : 2;
+    s.dk = a.dk + (kb * a.dkb + ks * a.dks + (int64_t)hkv * a.dkh) * ges;
+    s.dv = a.dv + (kb * a.dvb + ks * a.dvs + (int64_t)hkv * a.dvh) * ges;
+    return s;
+}
+
+template <bool IS_BF16>
+struct Ops {
+    typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
+    __device__ static __forceinline__ f32x16_t mfma(const op_t& x, const op_t& y, const f32x16_t& acc) {
+        if constexpr (IS_BF16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, acc, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, acc, 0, 0, 0);
+    }
+    // two floats rounded to 16 bits, packed
+    __device__ static __forceinline__ uint32_t pack(float x, float y) {
+        if constexpr (IS_BF16) {
+            typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 v2;
+            const v2 p = {(__bf16)x, (__bf16)y};
+            return __builtin_bit_cast(uint32_t, p);
+        } else {
+            typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 v2;
+            const v2 p = {(_Float16)x, (_Float16)y};
+            return __builtin_bit_cast(uint32_t, p);
+        }
+    }
+    __device__ static __forceinline__ float to_f(uint16_t h) {
+        if constexpr (IS_BF16)
+            return __uint_as_float((uint32_t)h << 16);
+        else
+            return (float)__builtin_bit_cast(_Float16, h);
+    }
+    // A/B operand of the 32x32x16 MFMA whose lanes hold rows r0..r0+3 and
+    // r0+8..r0+11 (this lane's k-slots) of column `col` of a row-major LDS
+    // tile with row stride `st` elements (two ds_read_b64_tr_b16: in each
+    // 16-lane group lane i addresses 4 elements of row i/4 and receives
+    // element i%16 of rows 0..3).
+    __device__ static __forceinline__ op_t load_tr(const uint16_t* tile, int st, int r0, int c0, int lane) {
+        const int tr_row = 4 * (lane >> 5) + ((lane & 15) >> 2);
+        const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const uint16_t* p0 = tile + (r0 + tr_row) * st + c0 + tr_col;
+        const uint16_t* p1 = p0 + 8 * st;
+        if constexpr (IS_BF16) {
+            typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 v4;
+            typedef __attribute__((address_space(3))) v4* lp;
+            const v4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p0));
+            const v4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lp)(p1));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+            typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4h;
+            typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 v4;
+            typedef __attribute__((address_space(3))) v4h* lp;
+            const v4 lo = __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p0)));
+            const v4 hi = __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p1)));
+            return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    }
+};
+
+// Soft-cap and ALiBi of one raw score (natural-log units), and the soft-cap
+// derivative factor 1 - tanh^2 (1 without soft-cap).
+template <bool BIAS>
+__device__ __forceinline__ float transform(const KArgs& f, float x, float slope, int dist, float& dcap) {
+    dcap = 1.f;
+    if constexpr (BIAS) {
+        x *= f.scale;
+        if (f.softcap > 0.f) {
+            // tanh(x / cap) = 1 - 2 / (exp(2x/cap) + 1)
+            const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(fast_exp2(x * f.softcap_k) + 1.f);
+            x = f.softcap * t;
+            dcap = 1.f - t * t;
+        }
+        if (f.alibi) x = fmaf(-slope, fabsf((float)dist), x);
+    }
+    return x;
+}
+
+// exp2-domain lse of a row for P = exp2(s*c - lse2): lse*log2(e), and +inf for
+// a row with no valid key (so its P is 0).
+__device__ __forceinline__ float lse2_of(float lse) { return lse == -INFINITY ? INFINITY : lse * kLog2e; }
+
+// ----------------------------------------------------------------------------
+// Dsum = rowsum(dO * O) in fp32: 16 lanes per row, 8 elements per lane.
+template <bool IS_BF16>
+__global__ void __launch_bounds__(kBThreads) mfa_bwd_dsum_kernel(BArgs a) {
+    const int bid = blockIdx.x;
+    const int unit = bid / a.T, tile = bid - unit * a.T;
+    const int b = unit / a.f.Hq, hq = unit - b * a.f.Hq;
+    const QView qv = q_view(a, b, hq);
+    const int row = tile * 16 + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+    float acc = 0.f;
+    const int d0 = sub * 8;
+    if (row < qv.Lq && d0 < a.f.D) {
+        const u32x4_t o = *reinterpret_cast<const u32x4_t*>(qv.o + ((int64_t)row * a.f.os + d0) * 2);
+        const u32x4_t g = *reinterpret_cast<const u32x4_t*>(qv.dout + ((int64_t)row * a.dos + d0) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = fmaf(Ops<IS_BF16>::to_f((uint16_t)(o[i] & 0xffff)), Ops<IS_BF16>::to_f((uint16_t)(g[i] & 0xffff)), acc);
+            acc = fmaf(Ops<IS_BF16>::to_f((uint16_t)(o[i] >> 16)), Ops<IS_BF16>::to_f((uint16_t)(g[i] >> 16)), acc);
+        }
+    }
+    acc += __shfl_xor(acc, 8);
+    acc += __shfl_xor(acc, 4);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 1);
+    if (sub == 0 && row < qv.Lq) qv.dsum[row] = acc;
+}
+
+// Store rows of a transposed accumulator (lane = row `idx` of the output,
+// registers = columns d = 32*db + 8*g + 4*half + 0..3), scaled.
+template <int DB>
+__device__ __forceinline__ void store_rows(char* base, int64_t row_stride, int D, bool f32out, bool is_bf16,
+                                           const f32x16_t (&acc)[DB], float scale, int half) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * db + 8 * g + 4 * half;
+            if (d >= D) continue;
+            const float v0 = acc[db][4 * g] * scale, v1 = acc[db][4 * g + 1] * scale;
+            const float v2 = acc[db][4 * g + 2] * scale, v3 = acc[db][4 * g + 3] * scale;
+            if (f32out) {
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(base) + d) = make_float4(v0, v1, v2, v3);
+            } else if (is_bf16) {
+                typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 v4;
+                const v4 w = {(__bf16)v0, (__bf16)v1, (__bf16)v2, (__bf16)v3};
+                *reinterpret_cast<v4*>(reinterpret_cast<__bf16*>(base) + d) = w;
+            } else {
+                typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 v4;
+                const v4 w = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+                *reinterpret_cast<v4*>(reinterpret_cast<_Float16*>(base) + d) = w;
+            }
+        }
+    (void)row_stride;
+}
+
+// ----------------------------------------------------------------------------
+// dK / dV: workgroup = 128 keys of one (sequence, K/V head), 32 per wavefront.
+template <int DP, bool IS_BF16, bool BIAS>
+__global__ void __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(1)))
+mfa_bwd_dkdv_kernel(BArgs a) {
+    typedef Ops<IS_BF16> O;
+    typedef typename O::op_t op_t;
+    constexpr int DS = DP / 16, DB = DP / 32;
+    constexpr int BQ = 32;       // query rows per step
+    constexpr int QST = DP + 8;  // LDS row stride of the Q / dO tiles (elements)
+    constexpr int CPR = DP / 8;  // 16-byte chunks per row
+    __shared__ __attribute__((aligned(16))) uint16_t q_s[BQ * QST];
+    __shared__ __attribute__((aligned(16))) uint16_t do_s[BQ * QST];
+    __shared__ __attribute__((aligned(16))) float lse_s[BQ];
+    __shared__ __attribute__((aligned(16))) float ds_s[BQ];
+
+    const KArgs& f = a.f;
+    const int bid = blockIdx.x;
+    const int ktile = bid / a.Ukv, unit = bid - ktile * a.Ukv;
+    const int b = unit / f.Hkv, hkv = unit - b * f.Hkv;
+    const KView kv = k_view(a, b, hkv);
+    const int Lk = kv.Lk, D = f.D;
+    const int k0 = ktile * 128;
+    if (k0 >= Lk) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int key = k0 + wave * 32 + l32;  // this lane's key (B-operand / accumulator column)
+    const int k1 = min(k0 + 128, Lk) - 1;
+
+    // K and V rows of this lane's key as B operands (k-slots d = 16*s + 8*half + 0..7)
+    op_t kf[DS], vf[DS];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+        const int d = 16 * s + 8 * half;
+        u32x4_t kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+        if (key < Lk && d < D) {
+            kk = *reinterpret_cast<const u32x4_t*>(kv.k + ((int64_t)key * f.ks + d) * 2);
+            vv = *reinterpret_cast<const u32x4_t*>(kv.v + ((int64_t)key * f.vs + d) * 2);
+        }
+        kf[s] = __builtin_bit_cast(op_t, kk);
+        vf[s] = __builtin_bit_cast(op_t, vv);
+    }
+    f32x16_t dka[DB], dva[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dka[db][r] = dva[db][r] = 0.f;
+    const float c = BIAS ? kLog2e : f.scale_log2;
+
+    const int R = f.Hq / f.Hkv;
+    for (int rr = 0; rr < R; ++rr) {
+        const int hq = hkv * R + rr;
+        const QView qv = q_view(a, b, hq);
+        const int Lq = qv.Lq;
+        const int dq = Lk - Lq;
+        const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
+        // queries whose valid key interval meets [k0, k1]
+        int qlo = 0, qhi = Lq - 1;
+        if (f.causal) qlo = max(qlo, k0 - dq);
+        if (f.wr >= 0) qlo = max(qlo, k0 - f.wr - dq);
+        if (f.wl >= 0) qhi = min(qhi, k1 + f.wl - dq);
+        for (int q0 = (qlo / BQ) * BQ; q0 <= qhi; q0 += BQ) {
+            __syncthreads();  // the previous step's LDS reads are done
+            for (int cc = tid; cc < 2 * BQ * CPR; cc += kBThreads) {
+                const int t = cc / (BQ * CPR), c2 = cc - t * (BQ * CPR);
+                const int row = c2 / CPR, col = (c2 % CPR) * 8;
+                u32x4_t val = {0, 0, 0, 0};
+                if (q0 + row < Lq && col < D) {
+                    const char* src = t == 0 ? qv.q + ((int64_t)(q0 + row) * f.qs + col) * 2
+                                             : qv.dout + ((int64_t)(q0 + row) * a.dos + col) * 2;
+                    val = *reinterpret_cast<const u32x4_t*>(src);
+                }
+                *reinterpret_cast<u32x4_t*>((t == 0 ? q_s : do_s) + row * QST + col) = val;
+            }
+            if (tid < BQ) {
+                const bool in = q0 + tid < Lq;
+                lse_s[tid] = in ? lse2_of(qv.lse[q0 + tid]) : INFINITY;
+                ds_s[tid] = in ? qv.dsum[q0 + tid] : 0.f;
+            }
+            __syncthreads();
+
+            // S = Q K^T and dP = dO V^T (lane = key, registers = query rows)
+            f32x16_t sacc, dpacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = dpacc[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < DS; ++s) {
+                const op_t qa = *reinterpret_cast<const op_t*>(q_s + l32 * QST + 16 * s + 8 * half);
+                const op_t da = *reinterpret_cast<const op_t*>(do_s + l32 * QST + 16 * s + 8 * half);
+                sacc = O::mfma(qa, kf[s], sacc);
+                dpacc = O::mfma(da, vf[s], dpacc);
+            }
+            // P and dS, rounded to 16 bits for the MFMAs; register r is query
+            // q0 + acc_row(r) + 4*half
+            uint32_t pw[8], dw[8];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 l4 = *reinterpret_cast<const float4*>(lse_s + 8 * g + 4 * half);
+                const float4 d4 = *reinterpret_cast<const float4*>(ds_s + 8 * g + 4 * half);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+                float p[4], ds[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * g + i;
+                    const int q = q0 + acc_row(r) + 4 * half;
+                    const int center = q + dq;
+                    float dcap;
+                    const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
+                    const bool ok = key <= key_hi(f, center, Lk) && key >= key_lo(f, center) && q < Lq;
+                    p[i] = ok ? fast_exp2(fmaf(x, c, -lv[i])) : 0.f;
+                    ds[i] = p[i] * (dpacc[r] - dv4[i]) * dcap;
+                }
+                pw[2 * g] = O::pack(p[0], p[1]);
+                pw[2 * g + 1] = O::pack(p[2], p[3]);
+                dw[2 * g] = O::pack(ds[0], ds[1]);
+                dw[2 * g + 1] = O::pack(ds[2], ds[3]);
+            }
+            // dV^T += dO^T P, dK^T += Q^T dS: k-slots = query rows of accumulator
+            // registers 8*st..8*st+7 (rows 16*st + 4*half + 0..3, +8..11)
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
+                const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const op_t dot = O::load_tr(do_s, QST, 16 * st, 32 * db, lane);
+                    const op_t qt = O::load_tr(q_s, QST, 16 * st, 32 * db, lane);
+                    dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
+                    dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
+                }
+            }
+        }
+    }
+    if (key < Lk) {
+        const bool f32o = a.grad_f32 != 0;
+        const int ges = f32o ? 4 : 2;
+        store_rows<DB>(kv.dk + (int64_t)key * a.dks * ges, 0, D, f32o, IS_BF16, dka, f.scale, half);
+        store_rows<DB>(kv.dv + (int64_t)key * a.dvs * ges, 0, D, f32o, IS_BF16, dva, 1.f, half);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// dQ: workgroup = 128 query rows of one (sequence, query head), 32 per wavefront.
+template <int DP, bool IS_BF16, bool BIAS>
+__global__ void __launch_bounds__(kBThreads) __attribute__((amdgpu_waves_per_eu(1)))
+mfa_bwd_dq_kernel(BArgs a) {
+    typedef Ops<IS_BF16> O;
+    typedef typename O::op_t op_t;
+    constexpr int DS = DP / 16, DB = DP / 32;
+    constexpr int BN = 64, NKB = 2;  // keys per block
+    constexpr int KST = DP + 8;
+    constexpr int CPR = DP / 8;
+    __shared__ __attribute__((aligned(16))) uint16_t k_s[BN * KST];
+    __shared__ __attribute__((aligned(16))) uint16_t v_s[BN * KST];
+
+    const KArgs& f = a.f;
+    const int bid = blockIdx.x;
+    const int tt = bid / f.U, unit = bid - tt * f.U;
+    const int tile = a.T - 1 - tt;  // heaviest (causal: last) query tiles first
+    const int b = unit / f.Hq, hq = unit - b * f.Hq;
+    const int hkv = hq / (f.Hq / f.Hkv);
+    const QView qv = q_view(a, b, hq);
+    const KView kv = k_view(a, b, hkv);
+    const int Lq = qv.Lq, Lk = kv.Lk, D = f.D;
+    const int q0 = tile * 128;
+    if (q0 >= Lq) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int dq = Lk - Lq;
+    const int q = q0 + wave * 32 + l32;  // this lane's query
+    const bool qin = q < Lq;
+
+    // Q and dO rows as B operands (k-slots d = 16*s + 8*half + 0..7)
+    op_t qf[DS], dof[DS];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+        const int d = 16 * s + 8 * half;
+        u32x4_t qq = {0, 0, 0, 0}, gg = {0, 0, 0, 0};
+        if (qin && d < D) {
+            qq = *reinterpret_cast<const u32x4_t*>(qv.q + ((int64_t)q * f.qs + d) * 2);
+            gg = *reinterpret_cast<const u32x4_t*>(qv.dout + ((int64_t)q * a.dos + d) * 2);
+        }
+        qf[s] = __builtin_bit_cast(op_t, qq);
+        dof[s] = __builtin_bit_cast(op_t, gg);
+    }
+    const float lse2 = qin ? lse2_of(qv.lse[q]) : INFINITY;
+    const float dsum = qin ? qv.dsum[q] : 0.f;
+    const int center = q + dq;
+    const int lo = key_lo(f, center), hi = key_hi(f, center, Lk);
+    const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
+    const float c = BIAS ? kLog2e : f.scale_log2;
+    f32x16_t dqa[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dqa[db][r] = 0.f;
+
+    // key blocks any row of the workgroup can see
+    const int qlast = min(q0 + 128, Lq) - 1;
+    const int klo = key_lo(f, q0 + dq);
+    const int khi = key_hi(f, qlast + dq, Lk);
+    const int jbeg = (klo / BN) * BN;
+    const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
+    for (int u = 0; u < nblk; ++u) {
+        const int j = jbeg + u * BN;
+        __syncthreads();
+        for (int cc = tid; cc < 2 * BN * CPR; cc += kBThreads) {
+            const int t = cc / (BN * CPR), c2 = cc - t * (BN * CPR);
+            const int row = c2 / CPR, col = (c2 % CPR) * 8;
+            u32x4_t val = {0, 0, 0, 0};
+            if (j + row < Lk && col < D) {
+                const char* src = t == 0 ? kv.k + ((int64_t)(j + row) * f.ks + col) * 2
+                                         : kv.v + ((int64_t)(j + row) * f.vs + col) * 2;
+                val = *reinterpret_cast<const u32x4_t*>(src);
+            }
+            *reinterpret_cast<u32x4_t*>((t == 0 ? k_s : v_s) + row * KST + col) = val;
+        }
+        __syncthreads();
+        uint32_t dw[NKB][8];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            // S^T = K Q^T and dP^T = V dO^T (lane = query, registers = keys)
+            f32x16_t sacc, dpacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = dpacc[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < DS; ++s) {
+                const op_t ka = *reinterpret_cast<const op_t*>(k_s + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                const op_t va = *reinterpret_cast<const op_t*>(v_s + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                sacc = O::mfma(ka, qf[s], sacc);
+                dpacc = O::mfma(va, dof[s], dpacc);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float ds2[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int key = j + 32 * kb + acc_row(r + i) + 4 * half;
+                    float dcap;
+                    const float x = transform<BIAS>(f, sacc[r + i], slope, center - key, dcap);
+                    const bool ok = key >= lo && key <= hi && qin;
+                    const float p = ok ? fast_exp2(fmaf(x, c, -lse2)) : 0.f;
+                    ds2[i] = p * (dpacc[r + i] - dsum) * dcap;
+                }
+                dw[kb][r / 2] = O::pack(ds2[0], ds2[1]);
+            }
+        }
+        // dQ^T += K^T dS^T (k-slots = keys of accumulator registers 8*st..8*st+7)
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const u32x4_t dsv = {dw[kb][4 * st], dw[kb][4 * st + 1], dw[kb][4 * st + 2], dw[kb][4 * st + 3]};
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const op_t kt = O::load_tr(k_s, KST, 32 * kb + 16 * st, 32 * db, lane);
+                    dqa[db] = O::mfma(kt, __builtin_bit_cast(op_t, dsv), dqa[db]);
+                }
+            }
+    }
+    if (qin) {
+        const bool f32o = a.grad_f32 != 0;
+        const int ges = f32o ? 4 : 2;
+        store_rows<DB>(qv.dq + (int64_t)q * a.dqs * ges, 0, D, f32o, IS_BF16, dqa, f.scale, half);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// host side
+
+int bset_err(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(mfa_error_buffer(), 512, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+typedef void (*bkernel_fn)(BArgs);
+
+struct BwdKernels {
+    bkernel_fn dsum, dkdv, dq;
+};
+
+template <int DP, bool IS_BF16>
+BwdKernels bwd_kernels(bool bias) {
+    BwdKernels k;
+    k.dsum = mfa_bwd_dsum_kernel<IS_BF16>;
+    k.dkdv = bias ? (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, true> : (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, false>;
+    k.dq = bias ? (bkernel_fn)mfa_bwd_dq_kernel<DP, IS_BF16, true> : (bkernel_fn)mfa_bwd_dq_kernel<DP, IS_BF16, false>;
+    return k;
+}
+template <bool IS_BF16>
+BwdKernels bwd_select(int dp, bool bias) {
+    switch (dp) {
+        case 32: return bwd_kernels<32, IS_BF16>(bias);
+        case 64: return bwd_kernels<64, IS_BF16>(bias);
+        case 96: return bwd_kernels<96, IS_BF16>(bias);
+        default: return bwd_kernels<128, IS_BF16>(bias);
+    }
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct BPlan {
+    BArgs a;
+    BwdKernels k;
+    int grid_dsum, grid_dkdv, grid_dq;
+    int64_t ws_bytes;
+    bool empty;
+};
+
+int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
+    if (!bp) return bset_err(MFA_ERR_INVALID, "mfa_bwd: params is NULL");
+    const mfa_fwd_params* p = &bp->fwd;
+    const int din = p->dtype_in;
+    if (din != MFA_DTYPE_F16 && din != MFA_DTYPE_BF16)
+        return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: dtype_in %d (the backward takes bf16/fp16)", din);
+    if (p->dtype_out != din)
+        return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: o and dout must have dtype_in");
+    if (bp->dtype_grad != din && bp->dtype_grad != MFA_DTYPE_F32)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: dtype_grad %d must equal dtype_in or be fp32", bp->dtype_grad);
+    const int D = p->head_dim;
+    if (D <= 0 || D > MFA_MAX_HEAD_DIM || D % 8 != 0)
+        return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: head_dim %d (a multiple of 8 up to %d)", D, MFA_MAX_HEAD_DIM);
+    if (p->batch < 0 || p->seqlen_q < 0 || p->seqlen_k < 0)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: negative batch/seqlen");
+    if (p->heads_q <= 0 || p->heads_kv <= 0 || p->heads_q % p->heads_kv != 0)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: num_heads_kv (%d) must divide num_heads_q (%d)", p->heads_kv,
+                        p->heads_q);
+    if (!(p->softcap >= 0.f)) return bset_err(MFA_ERR_INVALID, "mfa_bwd: softcap must be >= 0");
+    if (p->window_left < -1 || p->window_right < -1)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: window bounds must be >= -1");
+    if ((p->cu_seqlens_q == nullptr) != (p->cu_seqlens_k == nullptr))
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
+    if (p->block_table) return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: paged K/V (block_table) has no backward");
+    plan->empty = p->batch == 0 || p->seqlen_q == 0 || p->seqlen_k == 0;
+    if (!plan->empty) {
+        const void* ptrs[9] = {p->q, p->k, p->v, p->o, bp->dout, bp->dq, bp->dk, bp->dv, p->softmax_lse};
+        for (int i = 0; i < 9; ++i)
+            if (!ptrs[i]) return bset_err(MFA_ERR_INVALID, "mfa_bwd: NULL tensor pointer (softmax_lse is required)");
+        for (int i = 0; i < 8; ++i)
+            if (!al16(ptrs[i])) return bset_err(MFA_ERR_INVALID, "mfa_bwd: tensors must be 16-byte aligned");
+        const int64_t s16[15] = {p->q_batch_stride, p->q_seq_stride, p->q_head_stride, p->k_batch_stride,
+                                 p->k_seq_stride, p->k_head_stride, p->v_batch_stride, p->v_seq_stride,
+                                 p->v_head_stride, p->o_batch_stride, p->o_seq_stride, p->o_head_stride,
+                                 bp->do_batch_stride, bp->do_seq_stride, bp->do_head_stride};
+        for (int i = 0; i < 15; ++i)
+            if (s16[i] % 8 != 0)
+                return bset_err(MFA_ERR_INVALID, "mfa_bwd: q/k/v/o/dout strides must be multiples of 8 elements");
+        const int64_t sg[9] = {bp->dq_batch_stride, bp->dq_seq_stride, bp->dq_head_stride, bp->dk_batch_stride,
+                               bp->dk_seq_stride, bp->dk_head_stride, bp->dv_batch_stride, bp->dv_seq_stride,
+                               bp->dv_head_stride};
+        for (int i = 0; i < 9; ++i)
+            if (sg[i] % 4 != 0) return bset_err(MFA_ERR_INVALID, "mfa_bwd: dq/dk/dv strides must be multiples of 4 elements");
+        if (p->alibi_slopes && !(p->alibi_batch_stride == 0 || p->alibi_batch_stride == p->heads_q))
+            return bset_err(MFA_ERR_INVALID, "mfa_bwd: alibi_batch_stride must be 0 or heads_q");
+        if (p->lse_batch_stride < 0 || p->lse_head_stride < 0)
+            return bset_err(MFA_ERR_INVALID, "mfa_bwd: lse strides must be >= 0");
+    }
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128;
+    const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);
+    plan->k = din == MFA_DTYPE_BF16 ? bwd_select<true>(dp, bias) : bwd_select<false>(dp, bias);
+
+    BArgs& a = plan->a;
+    memset(&a, 0, sizeof(a));
+    KArgs& f = a.f;
+    f.q = static_cast<const char*>(p->q);
+    f.k = static_cast<const char*>(p->k);
+    f.v = static_cast<const char*>(p->v);
+    f.o = static_cast<char*>(p->o);
+    f.qb = p->q_batch_stride; f.qs = p->q_seq_stride; f.qh = p->q_head_stride;
+    f.kb = p->k_batch_stride; f.ks = p->k_seq_stride; f.kh = p->k_head_stride;
+    f.vb = p->v_batch_stride; f.vs = p->v_seq_stride; f.vh = p->v_head_stride;
+    f.ob = p->o_batch_stride; f.os = p->o_seq_stride; f.oh = p->o_head_stride;
+    f.cu_q = p->cu_seqlens_q;
+    f.cu_k = p->cu_seqlens_k;
+    f.alibi = p->alibi_slopes;
+    f.alibi_bstride = p->alibi_batch_stride;
+    f.B = p->batch; f.Hq = p->heads_q; f.Hkv = p->heads_kv;
+    f.Lq = p->seqlen_q; f.Lk = p->seqlen_k; f.D = D;
+    f.scale = p->scale;
+    f.scale_log2 = p->scale * kLog2e;
+    f.softcap = p->softcap;
+    f.softcap_k = p->softcap > 0.f ? 2.f * kLog2e / p->softcap : 0.f;
+    const int64_t wmax = (int64_t)p->seqlen_q + (int64_t)p->seqlen_k + 1;
+    f.wl = p->window_left < 0 ? -1 : (int32_t)(p->window_left > wmax ? wmax : p->window_left);
+    f.wr = p->window_right < 0 ? -1 : (int32_t)(p->window_right > wmax ? wmax : p->window_right);
+    f.causal = p->causal ? 1 : 0;
+    f.lse = p->softmax_lse;
+    f.lse_b = p->lse_batch_stride;
+    f.lse_h = p->lse_head_stride;
+    f.U = p->batch * p->heads_q;
+    f.npages = 1;
+    a.dout = static_cast<const char*>(bp->dout);
+    a.dob = bp->do_batch_stride; a.dos = bp->do_seq_stride; a.doh = bp->do_head_stride;
+    a.dq = static_cast<char*>(bp->dq);
+    a.dqb = bp->dq_batch_stride; a.dqs = bp->dq_seq_stride; a.dqh = bp->dq_head_stride;
+    a.dk = static_cast<char*>(bp->dk);
+    a.dkb = bp->dk_batch_stride; a.dks = bp->dk_seq_stride; a.dkh = bp->dk_head_stride;
+    a.dv = static_cast<char*>(bp->dv);
+    a.dvb = bp->dv_batch_stride; a.dvs = bp->dv_seq_stride; a.dvh = bp->dv_head_stride;
+    a.grad_f32 = bp->dtype_grad == MFA_DTYPE_F32 ? 1 : 0;
+    a.Ukv = p->batch * p->heads_kv;
+    const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
+    plan->ws_bytes = plan->empty ? 0 : ((rows * 4 + 255) / 256) * 256;
+    const int64_t g1 = (int64_t)f.U * ((p->seqlen_q + 15) / 16);
+    const int64_t g2 = (int64_t)a.Ukv * ((p->seqlen_k + 127) / 128);
+    const int64_t g3 = (int64_t)f.U * ((p->seqlen_q + 127) / 128);
+    if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: problem too large");
+    plan->grid_dsum = (int)g1;
+    plan->grid_dkdv = (int)g2;
+    plan->grid_dq = (int)g3;
+    return MFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfa_bwd_params_size(void) { return (int)sizeof(mfa_bwd_params); }
+
+int mfa_bwd_supported(int32_t dtype_in, int32_t head_dim) {
+    if (dtype_in != MFA_DTYPE_F16 && dtype_in != MFA_DTYPE_BF16) return 0;
+    return head_dim > 0 && head_dim <= MFA_MAX_HEAD_DIM && head_dim % 8 == 0;
+}
+
+int64_t mfa_bwd_workspace_bytes(const mfa_bwd_params* params) {
+    mfa_error_buffer()[0] = 0;
+    BPlan plan;
+    const int rc = make_bplan(params, &plan);
+    if (rc != MFA_OK) return rc;
+    return plan.ws_bytes;
+}
+
+int mfa_bwd(const mfa_bwd_params* params, void* workspace, int64_t workspace_bytes, void* stream) {
+    mfa_error_buffer()[0] = 0;
+    BPlan plan;
+    const int rc = make_bplan(params, &plan);
+    if (rc != MFA_OK) return rc;
+    if (plan.empty) return MFA_OK;
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: workspace must be a 256-byte aligned device pointer");
+    if (workspace_bytes < plan.ws_bytes)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                        (long long)plan.ws_bytes);
+    BArgs& a = plan.a;
+    a.dsum = static_cast<float*>(workspace);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    a.T = (params->fwd.seqlen_q + 15) / 16;
+    hipLaunchKernelGGL(plan.k.dsum, dim3(plan.grid_dsum), dim3(kBThreads), 0, st, a);
+    a.T = (params->fwd.seqlen_k + 127) / 128;
+    hipLaunchKernelGGL(plan.k.dkdv, dim3(plan.grid_dkdv), dim3(kBThreads), 0, st, a);
+    a.T = (params->fwd.seqlen_q + 127) / 128;
+    hipLaunchKernelGGL(plan.k.dq, dim3(plan.grid_dq), dim3(kBThreads), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return bset_err(MFA_ERR_LAUNCH, "mfa_bwd: launch failed: %s", hipGetErrorString(e));
+    return MFA_OK;
+}
+
+}  // extern "C"

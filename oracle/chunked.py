@@ -48,7 +48,7 @@ def broadcast_alibi(alibi_slopes, B, Hq):
 
 
 def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_right=-1, alibi=None,
-                chunk=DEFAULT_CHUNK, rows=None, return_lse=False):
+                chunk=DEFAULT_CHUNK, rows=None, return_lse=False, grad=False, dtype=torch.float32):
     """Heads-second q [B,Hq,Lq,D], k/v [B,Hkv,Lk,D] (CPU) -> fp32 [B,Hq,Lq,D].
 
     `alibi` is the broadcast [B*Hq] fp32 slope vector or None.  The result is
@@ -63,21 +63,27 @@ def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_righ
     torch.logsumexp(scores, -1) (-inf for a row whose keys are all masked).
     The reference computes but never returns this normaliser; it is the
     oracle of the build's softmax_lse output.
+
+    grad=True keeps q, k, v in the autograd graph (no detach; they must be CPU
+    tensors) so torch autograd gives the gradients of the reference's math --
+    the oracle of the build's backward; `dtype` is the compute precision
+    (float64 for gradcheck).
     """
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     if Hkv == 0 or Hq % Hkv != 0:
         raise ValueError(f"num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
-    qf = q.detach().cpu().float()
-    kf = k.detach().cpu().float()
-    vf = v.detach().cpu().float()
+    if grad:
+        qf, kf, vf = q.to(dtype), k.to(dtype), v.to(dtype)
+    else:
+        qf, kf, vf = (t.detach().cpu().to(dtype) for t in (q, k, v))
     if Hkv != Hq:
         rep = Hq // Hkv
         kf = kf.repeat_interleave(rep, dim=1)
         vf = vf.repeat_interleave(rep, dim=1)
     kt = kf.transpose(-1, -2)
-    out = torch.full((B, Hq, Lq, D), float("nan"), dtype=torch.float32)
-    lse = torch.full((B, Hq, Lq), float("nan"), dtype=torch.float32)
+    out = torch.full((B, Hq, Lq, D), float("nan"), dtype=dtype)
+    lse = torch.full((B, Hq, Lq), float("nan"), dtype=dtype)
     chunk = max(1, int(chunk))
     wl, wr = int(window_left), int(window_right)
     windowed = wl >= 0 or wr >= 0
@@ -92,7 +98,7 @@ def flash_torch(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_righ
         if alibi is not None:
             center_a = torch.arange(start, end)[:, None] + (Lk - Lq)
             key_a = torch.arange(Lk)[None, :]
-            scores = scores - alibi.reshape(B, Hq, 1, 1) * (center_a - key_a).abs().float()
+            scores = scores - alibi.to(dtype).reshape(B, Hq, 1, 1) * (center_a - key_a).abs().to(dtype)
         if causal or windowed:
             center = torch.arange(start, end)[:, None] + (Lk - Lq)
             if causal:
@@ -162,6 +168,48 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=No
         out[cu_q[i]:cu_q[i + 1]] = o[0].permute(1, 0, 2)
         lse[:, cu_q[i]:cu_q[i + 1]] = l[0]
     return (out, lse) if return_lse else out
+
+
+def attention_grads(q, k, v, dout, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
+                    alibi_slopes=None, dtype=torch.float32):
+    """Gradients (dq, dk, dv) of sum(out * dout) for heads-third q [B,Lq,Hq,D],
+    k/v [B,Lk,Hkv,D], by torch autograd through flash_torch (CPU, `dtype`).
+
+    The reference has no backward (metal_flash_attn/__init__.py:3-4); these
+    are the exact gradients of its forward math (_kernel.py:1165-1208), GQA
+    heads summed through repeat_interleave's backward.
+    """
+    B, _, Hq, D = q.shape
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    alibi = broadcast_alibi(alibi_slopes, B, Hq) if alibi_slopes is not None else None
+    qd, kd, vd = (t.detach().cpu().to(dtype).requires_grad_(True) for t in (q, k, v))
+    with torch.enable_grad():
+        out = flash_torch(qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), scale, causal, softcap,
+                          window_size[0], window_size[1], alibi, grad=True, dtype=dtype)
+        (out * dout.detach().cpu().to(dtype).transpose(1, 2)).sum().backward()
+    return qd.grad, kd.grad, vd.grad
+
+
+def attention_grads_varlen(q, k, v, dout, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, causal=False,
+                           window_size=(-1, -1), softcap=0.0, alibi_slopes=None, dtype=torch.float32):
+    """attention_grads for packed varlen q [Tq,Hq,D], k/v [Tk,Hkv,D] (one
+    sequence at a time, as flash_attn_varlen_func)."""
+    cu_q = [int(x) for x in torch.as_tensor(cu_seqlens_q).tolist()]
+    cu_k = [int(x) for x in torch.as_tensor(cu_seqlens_k).tolist()]
+    dq = torch.zeros(q.shape, dtype=dtype)
+    dk = torch.zeros(k.shape, dtype=dtype)
+    dv = torch.zeros(v.shape, dtype=dtype)
+    for i in range(len(cu_q) - 1):
+        a, b, c, d = cu_q[i], cu_q[i + 1], cu_k[i], cu_k[i + 1]
+        if b == a or d == c:
+            continue
+        seq_alibi = alibi_slopes
+        if alibi_slopes is not None and alibi_slopes.dim() == 2:
+            seq_alibi = alibi_slopes[i]
+        g = attention_grads(q[None, a:b], k[None, c:d], v[None, c:d], dout[None, a:b], softmax_scale, causal,
+                            window_size, softcap, seq_alibi, dtype)
+        dq[a:b], dk[c:d], dv[c:d] = g[0][0], g[1][0], g[2][0]
+    return dq, dk, dv
 
 
 def gather_pages(k_pages, block_table, seqlens_k):

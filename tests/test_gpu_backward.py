@@ -1,0 +1,199 @@
+"""GPU parity of the backward pass (dq, dk, dv through torch autograd and the
+mfa_bwd C ABI).  The reference is forward-only (metal_flash_attn/__init__.py:
+3-4), so the oracle is torch autograd through the restated forward
+(oracle.chunked.attention_grads, fp32 on the CPU), itself pinned against
+finite differences in test_oracle_pinning.py.
+
+Bar: every gradient within GRAD_REL * max|ref grad| of the oracle, judged on
+fp32 gradients (the C ABI's dtype_grad = fp32).  Beyond the forward's
+rounding of P to 16 bits, the backward rounds dS = P * (dP - Dsum) to 16 bits
+for the dQ and dK products, and Dsum comes from the forward output O rounded
+to 16 bits; the bar allows for those roundings (bf16: 2^-8 relative each).
+The bf16/fp16 gradients returned by autograd are held to twice that bar.
+Properties: two runs are bit-identical (no atomics), each varlen sequence's
+gradients equal its dense B=1 call bit for bit, grouped-query dK/dV equal
+the sum over the group's query heads of the repeated-K/V gradients (within
+the bar), and the SDPA patch carries gradients.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import mtlflashattn_amd as mfa
+from mtlflashattn_amd import _kernel
+from oracle import chunked
+from gpu_util import DEV, default_scale, make_qkv, make_varlen
+
+pytestmark = pytest.mark.gpu
+
+GRAD_REL = {torch.bfloat16: 6e-3, torch.float16: 1.5e-3}
+DTYPES16 = [torch.bfloat16, torch.float16]
+
+
+def grads_of(fn, q, k, v, dout):
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    out = fn(q, k, v)
+    out.backward(dout)
+    return out, q.grad, k.grad, v.grad
+
+
+def rel_err(got, ref):
+    ref = ref.float()
+    scale = max(ref.abs().max().item(), 1e-6)
+    return (got.detach().float().cpu() - ref).abs().max().item() / scale
+
+
+def check_grads(got, ref, dtype, what, factor=1.0):
+    for name, g, r in zip(("dq", "dk", "dv"), got, ref):
+        assert g.shape == r.shape, (what, name)
+        e = rel_err(g, r)
+        assert e <= factor * GRAD_REL[dtype], f"{what} {name}: rel err {e:.2e} > {factor * GRAD_REL[dtype]:.1e}"
+
+
+def fp32_grads(q, k, v, dout, scale, **kw):
+    """Gradients as fp32 straight from the C ABI (dtype_grad = fp32)."""
+    out, lse = _kernel.forward_bshd(q, k, v, scale, kw.get("causal", False), kw.get("softcap", 0.0),
+                                    kw.get("wl", -1), kw.get("wr", -1), kw.get("alibi"), return_lse=True)
+    alibi, bstride = _kernel._alibi_arg(kw.get("alibi"), q.shape[0], q.shape[2], q.device)
+    return _kernel._run_bwd(q, k, v, out, dout, lse, scale=scale, causal=kw.get("causal", False),
+                            softcap=kw.get("softcap", 0.0), window_left=kw.get("wl", -1),
+                            window_right=kw.get("wr", -1), alibi=alibi, alibi_bstride=bstride, grad_f32=True)
+
+
+FEATURES = [
+    dict(),
+    dict(causal=True),
+    dict(causal=True, window_size=(100, 0)),
+    dict(window_size=(60, 30)),
+    dict(softcap=5.0),
+    dict(alibi=True, causal=True),
+    dict(softcap=8.0, alibi=True, window_size=(90, 10)),
+    dict(softmax_scale=-0.09),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+@pytest.mark.parametrize("feat", FEATURES, ids=[str(i) for i in range(len(FEATURES))])
+@pytest.mark.parametrize("shape", [(2, 200, 333, 4, 2, 64), (1, 300, 150, 2, 2, 128)], ids=["lq<lk-gqa", "lq>lk-d128"])
+def test_grads_match_oracle(dtype, feat, shape):
+    B, Lq, Lk, Hq, Hkv, D = shape
+    q, k, v = make_qkv(B, Lq, Lk, Hq, Hkv, D, dtype, seed=Lq + D)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(7)).to(DEV, dtype)
+    kw = dict(feat)
+    if kw.pop("alibi", False):
+        kw["alibi_slopes"] = torch.linspace(0.05, 0.4, Hq, device=DEV)
+    out, *got = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, **kw), q, k, v, dout)
+    assert out.grad_fn is not None
+    ref = chunked.attention_grads(q, k, v, dout, kw.get("softmax_scale"), kw.get("causal", False),
+                                  kw.get("window_size", (-1, -1)), kw.get("softcap", 0.0),
+                                  kw["alibi_slopes"].cpu() if "alibi_slopes" in kw else None)
+    errs = [rel_err(g, r) for g, r in zip(got, ref)]
+    print(f"\n[bwd] {dtype} {feat} {shape} rel err dq/dk/dv (16-bit grads) = " + ", ".join(f"{e:.2e}" for e in errs))
+    check_grads(got, ref, dtype, f"{feat} {shape} 16-bit grads", factor=2.0)
+    scale = kw.get("softmax_scale") or default_scale(D)
+    ws = kw.get("window_size", (-1, -1))
+    g32 = fp32_grads(q, k, v, dout, scale, causal=kw.get("causal", False), softcap=kw.get("softcap", 0.0),
+                     wl=ws[0], wr=ws[1], alibi=kw.get("alibi_slopes"))
+    errs = [rel_err(g, r) for g, r in zip(g32, ref)]
+    print(f"[bwd] fp32 grads rel err = " + ", ".join(f"{e:.2e}" for e in errs))
+    check_grads(g32, ref, dtype, f"{feat} {shape} fp32 grads")
+
+
+@pytest.mark.parametrize("d", [8, 40, 96, 100])
+def test_head_dims(d):
+    q, k, v = make_qkv(1, 130, 170, 2, 1, d, torch.bfloat16, seed=d)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(8)).to(DEV, torch.bfloat16)
+    _, *got = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True), q, k, v, dout)
+    ref = chunked.attention_grads(q, k, v, dout, causal=True)
+    check_grads(got, ref, torch.bfloat16, f"D={d}", factor=2.0)
+
+
+def test_deterministic():
+    q, k, v = make_qkv(2, 257, 300, 4, 2, 64, torch.bfloat16, seed=9)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(9)).to(DEV, torch.bfloat16)
+    f = lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True)  # noqa: E731
+    a = grads_of(f, q, k, v, dout)
+    b = grads_of(f, q, k, v, dout)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+def test_varlen_grads(dtype):
+    lens_q, lens_k = [5, 0, 130, 1, 64], [9, 7, 200, 0, 64]
+    q, k, v, cu_q, cu_k = make_varlen(lens_q, lens_k, 4, 2, 64, dtype, seed=10)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(10)).to(DEV, dtype)
+    f = lambda q, k, v: mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens_q), max(lens_k),  # noqa: E731
+                                                   causal=True)
+    _, *got = grads_of(f, q, k, v, dout)
+    ref = chunked.attention_grads_varlen(q, k, v, dout, cu_q.cpu(), cu_k.cpu(), causal=True)
+    check_grads(got, ref, dtype, "varlen", factor=2.0)
+    # each sequence equals its dense B=1 call bit for bit
+    sq = [0] + torch.tensor(lens_q).cumsum(0).tolist()
+    sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()
+    for i in range(len(lens_q)):
+        if lens_q[i] == 0 or lens_k[i] == 0:
+            continue
+        a, b, c, d = sq[i], sq[i + 1], sk[i], sk[i + 1]
+        _, dq, dk, dv = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True),
+                                 q[None, a:b], k[None, c:d], v[None, c:d], dout[None, a:b])
+        assert torch.equal(got[0][a:b], dq[0]) and torch.equal(got[1][c:d], dk[0]) and \
+            torch.equal(got[2][c:d], dv[0]), f"sequence {i}"
+    # keys of a sequence whose queries are empty get zero gradients
+    assert (got[1][sk[1]:sk[2]] == 0).all() and (got[2][sk[1]:sk[2]] == 0).all()
+
+
+def test_packed_and_heads_second_paths_carry_gradients():
+    q, k, v = make_qkv(1, 100, 100, 4, 4, 64, torch.float16, seed=11)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(11)).to(DEV, torch.float16)
+    _, *ref = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True), q, k, v, dout)
+    qkv = torch.stack([q, k, v], dim=2).detach().requires_grad_(True)
+    mfa.flash_attn_qkvpacked_func(qkv, causal=True).backward(dout)
+    assert torch.equal(qkv.grad[:, :, 0], ref[0]) and torch.equal(qkv.grad[:, :, 1], ref[1])
+    _, *hs = grads_of(lambda q, k, v: mfa.flash_attn_forward(q.transpose(1, 2), k.transpose(1, 2),
+                                                             v.transpose(1, 2), default_scale(64), True)
+                      .transpose(1, 2), q, k, v, dout)
+    for a, b in zip(hs, ref):
+        assert torch.equal(a, b)
+
+
+def test_sdpa_patch_carries_gradients(monkeypatch):
+    from mtlflashattn_amd import sdpa
+    import torch.nn.functional as F
+
+    calls = []
+    real = _kernel._run_bwd
+    monkeypatch.setattr(_kernel, "_run_bwd", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+
+    q, k, v = (t.transpose(1, 2) for t in make_qkv(1, 600, 600, 4, 4, 64, torch.bfloat16, seed=12))
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(12)).to(DEV, torch.bfloat16)
+    sdpa.install()
+    try:
+        _, *got = grads_of(lambda q, k, v: F.scaled_dot_product_attention(q, k, v, is_causal=True), q, k, v, dout)
+    finally:
+        sdpa.uninstall()
+    ref = chunked.attention_grads(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), dout.transpose(1, 2),
+                                  causal=True)
+    assert calls, "the patched SDPA call did not run the HIP backward"
+    check_grads([g.transpose(1, 2) for g in got], ref, torch.bfloat16, "sdpa", factor=2.0)
+
+
+def test_fp32_backward_is_not_implemented():
+    q, k, v = make_qkv(1, 16, 16, 2, 2, 64, torch.float32, seed=13)
+    q.requires_grad_(True)
+    out = mfa.flash_attn_func(q, k, v)
+    with pytest.raises(NotImplementedError):
+        out.sum().backward()
+
+
+def test_gqa_grads_equal_summed_repeated_heads():
+    q, k, v = make_qkv(1, 150, 170, 8, 2, 64, torch.bfloat16, seed=14)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(14)).to(DEV, torch.bfloat16)
+    f = lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True)  # noqa: E731
+    _, dq, dk, dv = grads_of(f, q, k, v, dout)
+    _, dq_r, dk_r, dv_r = grads_of(f, q, k.repeat_interleave(4, dim=2), v.repeat_interleave(4, dim=2), dout)
+    assert torch.equal(dq, dq_r)  # the dQ kernel does the same arithmetic per query head
+    for g, r in ((dk, dk_r), (dv, dv_r)):
+        summed = r.float().reshape(1, 170, 2, 4, 64).sum(3)
+        assert rel_err(g, summed.cpu()) <= GRAD_REL[torch.bfloat16]

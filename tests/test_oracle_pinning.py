@@ -415,3 +415,64 @@ def test_gather_pages_follows_the_block_table():
     got = chunked.gather_pages(pool, table, [5, 0, 8])
     want = torch.tensor([200, 201, 202, 203, 0, 100, 101, 102, 103, 300, 301, 302, 303]).float()
     assert torch.equal(got[:, 0, 0], want) and torch.equal(got[:, 0, 1], want)
+
+
+# --------------------------------------------------------------------------- gradients (backward oracle)
+# The reference has no backward; the oracle's gradients are torch autograd
+# through the same restated forward, pinned here against finite differences
+# (torch.autograd.gradcheck, float64) and closed forms.
+
+GRAD_CASES = [
+    dict(),
+    dict(causal=True),
+    dict(causal=True, window_size=(2, 0)),
+    dict(window_size=(1, 2)),
+    dict(softcap=1.5),
+    dict(alibi=True, causal=True),
+    dict(softcap=3.0, alibi=True, window_size=(3, 1)),
+]
+
+
+@pytest.mark.parametrize("case", GRAD_CASES, ids=[str(i) for i in range(len(GRAD_CASES))])
+@pytest.mark.parametrize("shape", [(1, 5, 7, 2, 1, 8), (2, 6, 4, 2, 2, 8)], ids=["lq<lk-mqa", "lq>lk"])
+def test_gradients_match_finite_differences(case, shape):
+    B, Lq, Lk, Hq, Hkv, D = shape
+    g = torch.Generator().manual_seed(20)
+    q = torch.randn(B, Lq, Hq, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, Lk, Hkv, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, Lk, Hkv, D, generator=g, dtype=torch.float64)
+    kw = dict(case)
+    alibi = chunked.broadcast_alibi(torch.tensor([0.3, 0.7]).repeat(B, 1), B, Hq) if kw.pop("alibi", False) else None
+    ws = kw.pop("window_size", (-1, -1))
+
+    def f(q, k, v):
+        return chunked.flash_torch(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), 0.4,
+                                   kw.get("causal", False), kw.get("softcap", 0.0), ws[0], ws[1], alibi,
+                                   grad=True, dtype=torch.float64)
+
+    assert torch.autograd.gradcheck(f, tuple(t.requires_grad_(True) for t in (q, k, v)))
+
+
+def test_gradients_of_a_single_key_and_of_masked_rows():
+    # one key: out = v for every row, so dv = sum of dout over rows, dq = dk = 0
+    q, k, v = qkv(1, 2, 2, 6, 1, 8, seed=21)
+    dout = rnd(1, 6, 2, 8, seed=22)
+    dq, dk, dv = chunked.attention_grads(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), dout)
+    close(dq, torch.zeros_like(dq))
+    close(dk, torch.zeros_like(dk))
+    close(dv, dout.sum(dim=1, keepdim=True))
+    # causal Lq > Lk: the first Lq - Lk rows see no key and get no gradient
+    q, k, v = qkv(1, 2, 2, 7, 3, 8, seed=23)
+    dout = rnd(1, 7, 2, 8, seed=24)
+    dq, _, _ = chunked.attention_grads(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), dout, causal=True)
+    assert (dq[:, :4] == 0).all() and (dq[:, 4:] != 0).any()
+
+
+def test_fp32_gradients_agree_with_float64():
+    q, k, v = qkv(1, 4, 2, 33, 40, 16, seed=25)
+    dout = rnd(1, 33, 4, 16, seed=26)
+    args = (q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), dout)
+    g32 = chunked.attention_grads(*args, causal=True, softcap=5.0)
+    g64 = chunked.attention_grads(*args, causal=True, softcap=5.0, dtype=torch.float64)
+    for a, b in zip(g32, g64):
+        close(a, b, atol=2e-5)
