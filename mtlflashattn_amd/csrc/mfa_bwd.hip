@@ -261,10 +261,12 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     constexpr int BQ = 32;       // query rows per step
     constexpr int QST = DP + 8;  // LDS row stride of the Q / dO tiles (elements)
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
-    __shared__ __attribute__((aligned(16))) uint16_t q_s[BQ * QST];
-    __shared__ __attribute__((aligned(16))) uint16_t do_s[BQ * QST];
-    __shared__ __attribute__((aligned(16))) float lse_s[BQ];
-    __shared__ __attribute__((aligned(16))) float ds_s[BQ];
+    constexpr int SCH = (2 * BQ * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread
+    // two stages: the next query block is loaded while this one is computed
+    __shared__ __attribute__((aligned(16))) uint16_t q_s[2][BQ * QST];
+    __shared__ __attribute__((aligned(16))) uint16_t do_s[2][BQ * QST];
+    __shared__ __attribute__((aligned(16))) float lse_s[2][BQ];
+    __shared__ __attribute__((aligned(16))) float ds_s[2][BQ];
 
     const KArgs& f = a.f;
     const int bid = blockIdx.x;
@@ -299,37 +301,74 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         for (int r = 0; r < 16; ++r) dka[db][r] = dva[db][r] = 0.f;
     const float c = BIAS ? kLog2e : f.scale_log2;
 
+    // Query blocks: every head of the K/V group, the blocks whose rows can
+    // see [k0, k1] (the same range for every head: lengths are per sequence).
     const int R = f.Hq / f.Hkv;
-    for (int rr = 0; rr < R; ++rr) {
-        const int hq = hkv * R + rr;
-        const QView qv = q_view(a, b, hq);
-        const int Lq = qv.Lq;
-        const int dq = Lk - Lq;
-        const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
-        // queries whose valid key interval meets [k0, k1]
-        int qlo = 0, qhi = Lq - 1;
-        if (f.causal) qlo = max(qlo, k0 - dq);
-        if (f.wr >= 0) qlo = max(qlo, k0 - f.wr - dq);
-        if (f.wl >= 0) qhi = min(qhi, k1 + f.wl - dq);
-        for (int q0 = (qlo / BQ) * BQ; q0 <= qhi; q0 += BQ) {
-            __syncthreads();  // the previous step's LDS reads are done
-            for (int cc = tid; cc < 2 * BQ * CPR; cc += kBThreads) {
+    const int Lq = f.cu_q ? f.cu_q[b + 1] - f.cu_q[b] : f.Lq;
+    const int dq = Lk - Lq;
+    int qlo = 0, qhi = Lq - 1;
+    if (f.causal) qlo = max(qlo, k0 - dq);
+    if (f.wr >= 0) qlo = max(qlo, k0 - f.wr - dq);
+    if (f.wl >= 0) qhi = min(qhi, k1 + f.wl - dq);
+    const int qb0 = (qlo / BQ) * BQ;
+    const int nqb = qhi >= qb0 ? (qhi - qb0) / BQ + 1 : 0;
+    const int nsteps = R * nqb;
+
+    u32x4_t sreg[SCH];
+    float lreg = INFINITY, dreg = 0.f;
+    auto gload = [&](int step) {
+        const int rr = step / nqb;
+        const int q0 = qb0 + (step - rr * nqb) * BQ;
+        const QView qv = q_view(a, b, hkv * R + rr);
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) {
+            const int cc = tid + kBThreads * i;
+            const int t = cc / (BQ * CPR), c2 = cc - t * (BQ * CPR);
+            const int row = c2 / CPR, col = (c2 % CPR) * 8;
+            u32x4_t val = {0, 0, 0, 0};
+            if (cc < 2 * BQ * CPR && q0 + row < Lq && col < D) {
+                const char* src = t == 0 ? qv.q + ((int64_t)(q0 + row) * f.qs + col) * 2
+                                         : qv.dout + ((int64_t)(q0 + row) * a.dos + col) * 2;
+                val = *reinterpret_cast<const u32x4_t*>(src);
+            }
+            sreg[i] = val;
+        }
+        if (tid < BQ) {
+            const bool in = q0 + tid < Lq;
+            lreg = in ? lse2_of(qv.lse[q0 + tid]) : INFINITY;
+            dreg = in ? qv.dsum[q0 + tid] : 0.f;
+        }
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) {
+            const int cc = tid + kBThreads * i;
+            if (cc < 2 * BQ * CPR) {
                 const int t = cc / (BQ * CPR), c2 = cc - t * (BQ * CPR);
                 const int row = c2 / CPR, col = (c2 % CPR) * 8;
-                u32x4_t val = {0, 0, 0, 0};
-                if (q0 + row < Lq && col < D) {
-                    const char* src = t == 0 ? qv.q + ((int64_t)(q0 + row) * f.qs + col) * 2
-                                             : qv.dout + ((int64_t)(q0 + row) * a.dos + col) * 2;
-                    val = *reinterpret_cast<const u32x4_t*>(src);
-                }
-                *reinterpret_cast<u32x4_t*>((t == 0 ? q_s : do_s) + row * QST + col) = val;
+                *reinterpret_cast<u32x4_t*>((t == 0 ? q_s[buf] : do_s[buf]) + row * QST + col) = sreg[i];
             }
-            if (tid < BQ) {
-                const bool in = q0 + tid < Lq;
-                lse_s[tid] = in ? lse2_of(qv.lse[q0 + tid]) : INFINITY;
-                ds_s[tid] = in ? qv.dsum[q0 + tid] : 0.f;
-            }
-            __syncthreads();
+        }
+        if (tid < BQ) {
+            lse_s[buf][tid] = lreg;
+            ds_s[buf][tid] = dreg;
+        }
+    };
+    if (nsteps > 0) {
+        gload(0);
+        swrite(0);
+    }
+    __syncthreads();
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1;
+        if (step + 1 < nsteps) gload(step + 1);  // in flight during this step's MFMAs
+        const int rr = step / nqb;
+        const int q0 = qb0 + (step - rr * nqb) * BQ;
+        const int hq = hkv * R + rr;
+        const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
+        {
+            const uint16_t* qsb = q_s[buf];
+            const uint16_t* dosb = do_s[buf];
 
             // S = Q K^T and dP = dO V^T (lane = key, registers = query rows)
             f32x16_t sacc, dpacc;
@@ -337,37 +376,50 @@ mfa_bwd_dkdv_kernel(BArgs a) {
             for (int r = 0; r < 16; ++r) sacc[r] = dpacc[r] = 0.f;
 #pragma unroll
             for (int s = 0; s < DS; ++s) {
-                const op_t qa = *reinterpret_cast<const op_t*>(q_s + l32 * QST + 16 * s + 8 * half);
-                const op_t da = *reinterpret_cast<const op_t*>(do_s + l32 * QST + 16 * s + 8 * half);
+                const op_t qa = *reinterpret_cast<const op_t*>(qsb + l32 * QST + 16 * s + 8 * half);
+                const op_t da = *reinterpret_cast<const op_t*>(dosb + l32 * QST + 16 * s + 8 * half);
                 sacc = O::mfma(qa, kf[s], sacc);
                 dpacc = O::mfma(da, vf[s], dpacc);
             }
             // P and dS, rounded to 16 bits for the MFMAs; register r is query
-            // q0 + acc_row(r) + 4*half
+            // q0 + acc_row(r) + 4*half.  Tiles whose 32 x 32 pairs are all valid
+            // (wave-uniform test; lo/hi grow with the query) skip the masks.
+            const int wk0 = k0 + wave * 32;
+            const bool full = q0 + BQ <= Lq && key_lo(f, q0 + BQ - 1 + dq) <= wk0 && key_hi(f, q0 + dq, Lk) >= wk0 + 31;
             uint32_t pw[8], dw[8];
+            auto probs = [&](auto masked_tag) {
+                constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 l4 = *reinterpret_cast<const float4*>(lse_s + 8 * g + 4 * half);
-                const float4 d4 = *reinterpret_cast<const float4*>(ds_s + 8 * g + 4 * half);
-                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-                float p[4], ds[4];
+                for (int g = 0; g < 4; ++g) {
+                    const float4 l4 = *reinterpret_cast<const float4*>(lse_s[buf] + 8 * g + 4 * half);
+                    const float4 d4 = *reinterpret_cast<const float4*>(ds_s[buf] + 8 * g + 4 * half);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+                    float p[4], ds[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 4 * g + i;
-                    const int q = q0 + acc_row(r) + 4 * half;
-                    const int center = q + dq;
-                    float dcap;
-                    const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
-                    const bool ok = key <= key_hi(f, center, Lk) && key >= key_lo(f, center) && q < Lq;
-                    p[i] = ok ? fast_exp2(fmaf(x, c, -lv[i])) : 0.f;
-                    ds[i] = p[i] * (dpacc[r] - dv4[i]) * dcap;
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = 4 * g + i;
+                        const int q = q0 + acc_row(r) + 4 * half;
+                        const int center = q + dq;
+                        float dcap;
+                        const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
+                        bool ok = true;
+                        if constexpr (MASKED)
+                            ok = key <= key_hi(f, center, Lk) && key >= key_lo(f, center) && q < Lq;
+                        p[i] = ok ? fast_exp2(fmaf(x, c, -lv[i])) : 0.f;
+                        ds[i] = p[i] * (dpacc[r] - dv4[i]);
+                        if constexpr (BIAS) ds[i] *= dcap;
+                    }
+                    pw[2 * g] = O::pack(p[0], p[1]);
+                    pw[2 * g + 1] = O::pack(p[2], p[3]);
+                    dw[2 * g] = O::pack(ds[0], ds[1]);
+                    dw[2 * g + 1] = O::pack(ds[2], ds[3]);
                 }
-                pw[2 * g] = O::pack(p[0], p[1]);
-                pw[2 * g + 1] = O::pack(p[2], p[3]);
-                dw[2 * g] = O::pack(ds[0], ds[1]);
-                dw[2 * g + 1] = O::pack(ds[2], ds[3]);
-            }
+            };
+            if (full)
+                probs(std::false_type{});
+            else
+                probs(std::true_type{});
             // dV^T += dO^T P, dK^T += Q^T dS: k-slots = query rows of accumulator
             // registers 8*st..8*st+7 (rows 16*st + 4*half + 0..3, +8..11)
 #pragma unroll
@@ -376,13 +428,15 @@ mfa_bwd_dkdv_kernel(BArgs a) {
                 const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
-                    const op_t dot = O::load_tr(do_s, QST, 16 * st, 32 * db, lane);
-                    const op_t qt = O::load_tr(q_s, QST, 16 * st, 32 * db, lane);
+                    const op_t dot = O::load_tr(dosb, QST, 16 * st, 32 * db, lane);
+                    const op_t qt = O::load_tr(qsb, QST, 16 * st, 32 * db, lane);
                     dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
                     dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
                 }
             }
         }
+        if (step + 1 < nsteps) swrite(buf ^ 1);  // the other stage was last read before the previous barrier
+        __syncthreads();
     }
     if (key < Lk) {
         const bool f32o = a.grad_f32 != 0;
@@ -403,8 +457,9 @@ mfa_bwd_dq_kernel(BArgs a) {
     constexpr int BN = 64, NKB = 2;  // keys per block
     constexpr int KST = DP + 8;
     constexpr int CPR = DP / 8;
-    __shared__ __attribute__((aligned(16))) uint16_t k_s[BN * KST];
-    __shared__ __attribute__((aligned(16))) uint16_t v_s[BN * KST];
+    constexpr int SCH = (2 * BN * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread
+    __shared__ __attribute__((aligned(16))) uint16_t k_s[2][BN * KST];
+    __shared__ __attribute__((aligned(16))) uint16_t v_s[2][BN * KST];
 
     const KArgs& f = a.f;
     const int bid = blockIdx.x;
@@ -420,7 +475,8 @@ mfa_bwd_dq_kernel(BArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
     const int dq = Lk - Lq;
-    const int q = q0 + wave * 32 + l32;  // this lane's query
+    const int wq0 = q0 + wave * 32;      // first query row of this wavefront
+    const int q = wq0 + l32;             // this lane's query
     const bool qin = q < Lq;
 
     // Q and dO rows as B operands (k-slots d = 16*s + 8*half + 0..7)
@@ -454,21 +510,45 @@ mfa_bwd_dq_kernel(BArgs a) {
     const int khi = key_hi(f, qlast + dq, Lk);
     const int jbeg = (klo / BN) * BN;
     const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
-    for (int u = 0; u < nblk; ++u) {
+    u32x4_t sreg[SCH];
+    auto gload = [&](int u) {
         const int j = jbeg + u * BN;
-        __syncthreads();
-        for (int cc = tid; cc < 2 * BN * CPR; cc += kBThreads) {
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) {
+            const int cc = tid + kBThreads * i;
             const int t = cc / (BN * CPR), c2 = cc - t * (BN * CPR);
             const int row = c2 / CPR, col = (c2 % CPR) * 8;
             u32x4_t val = {0, 0, 0, 0};
-            if (j + row < Lk && col < D) {
+            if (cc < 2 * BN * CPR && j + row < Lk && col < D) {
                 const char* src = t == 0 ? kv.k + ((int64_t)(j + row) * f.ks + col) * 2
                                          : kv.v + ((int64_t)(j + row) * f.vs + col) * 2;
                 val = *reinterpret_cast<const u32x4_t*>(src);
             }
-            *reinterpret_cast<u32x4_t*>((t == 0 ? k_s : v_s) + row * KST + col) = val;
+            sreg[i] = val;
         }
-        __syncthreads();
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) {
+            const int cc = tid + kBThreads * i;
+            if (cc < 2 * BN * CPR) {
+                const int t = cc / (BN * CPR), c2 = cc - t * (BN * CPR);
+                const int row = c2 / CPR, col = (c2 % CPR) * 8;
+                *reinterpret_cast<u32x4_t*>((t == 0 ? k_s[buf] : v_s[buf]) + row * KST + col) = sreg[i];
+            }
+        }
+    };
+    if (nblk > 0) {
+        gload(0);
+        swrite(0);
+    }
+    __syncthreads();
+    for (int u = 0; u < nblk; ++u) {
+        const int j = jbeg + u * BN;
+        const int buf = u & 1;
+        if (u + 1 < nblk) gload(u + 1);  // in flight during this block's MFMAs
+        const uint16_t* ksb = k_s[buf];
+        const uint16_t* vsb = v_s[buf];
         uint32_t dw[NKB][8];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
@@ -478,25 +558,37 @@ mfa_bwd_dq_kernel(BArgs a) {
             for (int r = 0; r < 16; ++r) sacc[r] = dpacc[r] = 0.f;
 #pragma unroll
             for (int s = 0; s < DS; ++s) {
-                const op_t ka = *reinterpret_cast<const op_t*>(k_s + (32 * kb + l32) * KST + 16 * s + 8 * half);
-                const op_t va = *reinterpret_cast<const op_t*>(v_s + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                const op_t ka = *reinterpret_cast<const op_t*>(ksb + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                const op_t va = *reinterpret_cast<const op_t*>(vsb + (32 * kb + l32) * KST + 16 * s + 8 * half);
                 sacc = O::mfma(ka, qf[s], sacc);
                 dpacc = O::mfma(va, dof[s], dpacc);
             }
+            // tiles whose 32 x 32 pairs are all valid skip the masks
+            const int kk0 = j + 32 * kb;
+            const bool full = wq0 + 31 < Lq && key_lo(f, wq0 + 31 + dq) <= kk0 && key_hi(f, wq0 + dq, Lk) >= kk0 + 31;
+            auto dsrow = [&](auto masked_tag) {
+                constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                float ds2[2];
+                for (int r = 0; r < 16; r += 2) {
+                    float ds2[2];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int key = j + 32 * kb + acc_row(r + i) + 4 * half;
-                    float dcap;
-                    const float x = transform<BIAS>(f, sacc[r + i], slope, center - key, dcap);
-                    const bool ok = key >= lo && key <= hi && qin;
-                    const float p = ok ? fast_exp2(fmaf(x, c, -lse2)) : 0.f;
-                    ds2[i] = p * (dpacc[r + i] - dsum) * dcap;
+                    for (int i = 0; i < 2; ++i) {
+                        const int key = kk0 + acc_row(r + i) + 4 * half;
+                        float dcap;
+                        const float x = transform<BIAS>(f, sacc[r + i], slope, center - key, dcap);
+                        bool ok = true;
+                        if constexpr (MASKED) ok = key >= lo && key <= hi && qin;
+                        const float p = ok ? fast_exp2(fmaf(x, c, -lse2)) : 0.f;
+                        ds2[i] = p * (dpacc[r + i] - dsum);
+                        if constexpr (BIAS) ds2[i] *= dcap;
+                    }
+                    dw[kb][r / 2] = O::pack(ds2[0], ds2[1]);
                 }
-                dw[kb][r / 2] = O::pack(ds2[0], ds2[1]);
-            }
+            };
+            if (full)
+                dsrow(std::false_type{});
+            else
+                dsrow(std::true_type{});
         }
         // dQ^T += K^T dS^T (k-slots = keys of accumulator registers 8*st..8*st+7)
 #pragma unroll
@@ -506,10 +598,12 @@ mfa_bwd_dq_kernel(BArgs a) {
                 const u32x4_t dsv = {dw[kb][4 * st], dw[kb][4 * st + 1], dw[kb][4 * st + 2], dw[kb][4 * st + 3]};
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
-                    const op_t kt = O::load_tr(k_s, KST, 32 * kb + 16 * st, 32 * db, lane);
+                    const op_t kt = O::load_tr(ksb, KST, 32 * kb + 16 * st, 32 * db, lane);
                     dqa[db] = O::mfma(kt, __builtin_bit_cast(op_t, dsv), dqa[db]);
                 }
             }
+        if (u + 1 < nblk) swrite(buf ^ 1);
+        __syncthreads();
     }
     if (qin) {
         const bool f32o = a.grad_f32 != 0;
