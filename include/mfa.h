@@ -1,6 +1,6 @@
 /*
- * mfa.h -- C ABI of the MI355X (gfx950) flash-attention forward library
- * (libmtlfa_hip.so, built from mtlflashattn_amd/csrc/mfa_fwd.hip).
+ * mfa.h -- C ABI of the MI355X (gfx950) flash-attention library
+ * (libmtlfa_hip.so, built from mtlflashattn_amd/csrc/mfa_fwd.hip and mfa_bwd.hip).
  *
  * This is the drop-in boundary that replaces the reference's per-tier Metal
  * launch calls.  In the reference the Python launcher binds a JIT-compiled
