@@ -261,7 +261,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     constexpr int BQ = 32;       // query rows per step
     constexpr int QST = DP + 8;  // LDS row stride of the Q / dO tiles (elements)
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
-    constexpr int SCH = (2 * BQ * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread
+    constexpr int SCH = (BQ * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread and tensor
     // two stages: the next query block is loaded while this one is computed
     __shared__ __attribute__((aligned(16))) uint16_t q_s[2][BQ * QST];
     __shared__ __attribute__((aligned(16))) uint16_t do_s[2][BQ * QST];
@@ -314,24 +314,35 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     const int nqb = qhi >= qb0 ? (qhi - qb0) / BQ + 1 : 0;
     const int nsteps = R * nqb;
 
-    u32x4_t sreg[SCH];
+    // Staging through buffer loads: one resource per tensor and block, sized
+    // to the block's valid rows (rows past the sequence and chunks past the
+    // head dim read zero), so the loads carry no per-chunk conditions.
+    u32x4_t sq[SCH], sd[SCH];
+    uint32_t qoff[SCH], dooff[SCH];
+    int soff[SCH];
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+        const int cc = tid + kBThreads * i;
+        const int row = cc / CPR, col = (cc % CPR) * 8;
+        const bool in = cc < BQ * CPR && col < D;
+        qoff[i] = in ? (uint32_t)(((int64_t)row * f.qs + col) * 2) : 0x80000000u;
+        dooff[i] = in ? (uint32_t)(((int64_t)row * a.dos + col) * 2) : 0x80000000u;
+        soff[i] = row * QST + col;
+    }
     float lreg = INFINITY, dreg = 0.f;
     auto gload = [&](int step) {
         const int rr = step / nqb;
         const int q0 = qb0 + (step - rr * nqb) * BQ;
         const QView qv = q_view(a, b, hkv * R + rr);
+        const int rm1 = min(Lq - q0, BQ) - 1;  // q0 < Lq
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(qv.q + (int64_t)q0 * f.qs * 2), (short)0, (int)(((int64_t)rm1 * f.qs + D) * 2), kBufferDword3);
+        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(qv.dout + (int64_t)q0 * a.dos * 2), (short)0, (int)(((int64_t)rm1 * a.dos + D) * 2), kBufferDword3);
 #pragma unroll
         for (int i = 0; i < SCH; ++i) {
-            const int cc = tid + kBThreads * i;
-            const int t = cc / (BQ * CPR), c2 = cc - t * (BQ * CPR);
-            const int row = c2 / CPR, col = (c2 % CPR) * 8;
-            u32x4_t val = {0, 0, 0, 0};
-            if (cc < 2 * BQ * CPR && q0 + row < Lq && col < D) {
-                const char* src = t == 0 ? qv.q + ((int64_t)(q0 + row) * f.qs + col) * 2
-                                         : qv.dout + ((int64_t)(q0 + row) * a.dos + col) * 2;
-                val = *reinterpret_cast<const u32x4_t*>(src);
-            }
-            sreg[i] = val;
+            sq[i] = __builtin_amdgcn_raw_buffer_load_b128(qr, qoff[i], 0, 0);
+            sd[i] = __builtin_amdgcn_raw_buffer_load_b128(dr, dooff[i], 0, 0);
         }
         if (tid < BQ) {
             const bool in = q0 + tid < Lq;
@@ -342,11 +353,9 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     auto swrite = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < SCH; ++i) {
-            const int cc = tid + kBThreads * i;
-            if (cc < 2 * BQ * CPR) {
-                const int t = cc / (BQ * CPR), c2 = cc - t * (BQ * CPR);
-                const int row = c2 / CPR, col = (c2 % CPR) * 8;
-                *reinterpret_cast<u32x4_t*>((t == 0 ? q_s[buf] : do_s[buf]) + row * QST + col) = sreg[i];
+            if (SCH * kBThreads == BQ * CPR || tid + kBThreads * i < BQ * CPR) {
+                *reinterpret_cast<u32x4_t*>(q_s[buf] + soff[i]) = sq[i];
+                *reinterpret_cast<u32x4_t*>(do_s[buf] + soff[i]) = sd[i];
             }
         }
         if (tid < BQ) {
@@ -457,7 +466,7 @@ mfa_bwd_dq_kernel(BArgs a) {
     constexpr int BN = 64, NKB = 2;  // keys per block
     constexpr int KST = DP + 8;
     constexpr int CPR = DP / 8;
-    constexpr int SCH = (2 * BN * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread
+    constexpr int SCH = (BN * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread and tensor
     __shared__ __attribute__((aligned(16))) uint16_t k_s[2][BN * KST];
     __shared__ __attribute__((aligned(16))) uint16_t v_s[2][BN * KST];
 
@@ -510,31 +519,38 @@ mfa_bwd_dq_kernel(BArgs a) {
     const int khi = key_hi(f, qlast + dq, Lk);
     const int jbeg = (klo / BN) * BN;
     const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
-    u32x4_t sreg[SCH];
+    // buffer-load staging as in the dK/dV kernel (rows past the sequence read zero)
+    u32x4_t sk[SCH], sv2[SCH];
+    uint32_t koff[SCH], voff[SCH];
+    int soff[SCH];
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+        const int cc = tid + kBThreads * i;
+        const int row = cc / CPR, col = (cc % CPR) * 8;
+        const bool in = cc < BN * CPR && col < D;
+        koff[i] = in ? (uint32_t)(((int64_t)row * f.ks + col) * 2) : 0x80000000u;
+        voff[i] = in ? (uint32_t)(((int64_t)row * f.vs + col) * 2) : 0x80000000u;
+        soff[i] = row * KST + col;
+    }
     auto gload = [&](int u) {
         const int j = jbeg + u * BN;
+        const int rm1 = min(Lk - j, BN) - 1;  // j < Lk
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kv.k + (int64_t)j * f.ks * 2), (short)0, (int)(((int64_t)rm1 * f.ks + D) * 2), kBufferDword3);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(kv.v + (int64_t)j * f.vs * 2), (short)0, (int)(((int64_t)rm1 * f.vs + D) * 2), kBufferDword3);
 #pragma unroll
         for (int i = 0; i < SCH; ++i) {
-            const int cc = tid + kBThreads * i;
-            const int t = cc / (BN * CPR), c2 = cc - t * (BN * CPR);
-            const int row = c2 / CPR, col = (c2 % CPR) * 8;
-            u32x4_t val = {0, 0, 0, 0};
-            if (cc < 2 * BN * CPR && j + row < Lk && col < D) {
-                const char* src = t == 0 ? kv.k + ((int64_t)(j + row) * f.ks + col) * 2
-                                         : kv.v + ((int64_t)(j + row) * f.vs + col) * 2;
-                val = *reinterpret_cast<const u32x4_t*>(src);
-            }
-            sreg[i] = val;
+            sk[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
+            sv2[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0);
         }
     };
     auto swrite = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < SCH; ++i) {
-            const int cc = tid + kBThreads * i;
-            if (cc < 2 * BN * CPR) {
-                const int t = cc / (BN * CPR), c2 = cc - t * (BN * CPR);
-                const int row = c2 / CPR, col = (c2 % CPR) * 8;
-                *reinterpret_cast<u32x4_t*>((t == 0 ? k_s[buf] : v_s[buf]) + row * KST + col) = sreg[i];
+            if (SCH * kBThreads == BN * CPR || tid + kBThreads * i < BN * CPR) {
+                *reinterpret_cast<u32x4_t*>(k_s[buf] + soff[i]) = sk[i];
+                *reinterpret_cast<u32x4_t*>(v_s[buf] + soff[i]) = sv2[i];
             }
         }
     };
@@ -704,6 +720,11 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
             return bset_err(MFA_ERR_INVALID, "mfa_bwd: alibi_batch_stride must be 0 or heads_q");
         if (p->lse_batch_stride < 0 || p->lse_head_stride < 0)
             return bset_err(MFA_ERR_INVALID, "mfa_bwd: lse strides must be >= 0");
+        // staged blocks (up to 64 rows) are addressed with 32-bit byte offsets
+        const int64_t rs[4] = {p->q_seq_stride, bp->do_seq_stride, p->k_seq_stride, p->v_seq_stride};
+        for (int i = 0; i < 4; ++i)
+            if (rs[i] < 0 || (63 * rs[i] + D) * 2 >= ((int64_t)1 << 31))
+                return bset_err(MFA_ERR_INVALID, "mfa_bwd: sequence strides must be >= 0 and span < 2 GiB per 64 rows");
     }
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128;
     const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);
