@@ -412,10 +412,12 @@ mfa_bwd_dkdv_kernel(BArgs a) {
                         const int center = q + dq;
                         float dcap;
                         const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
+                        // (bitwise tests and an unconditional exp: selects, no branches)
+                        const float pe = fast_exp2(fmaf(x, c, -lv[i]));
                         bool ok = true;
                         if constexpr (MASKED)
-                            ok = key <= key_hi(f, center, Lk) && key >= key_lo(f, center) && q < Lq;
-                        p[i] = ok ? fast_exp2(fmaf(x, c, -lv[i])) : 0.f;
+                            ok = (key <= key_hi(f, center, Lk)) & (key >= key_lo(f, center)) & (q < Lq);
+                        p[i] = ok ? pe : 0.f;
                         ds[i] = p[i] * (dpacc[r] - dv4[i]);
                         if constexpr (BIAS) ds[i] *= dcap;
                     }
@@ -592,9 +594,10 @@ mfa_bwd_dq_kernel(BArgs a) {
                         const int key = kk0 + acc_row(r + i) + 4 * half;
                         float dcap;
                         const float x = transform<BIAS>(f, sacc[r + i], slope, center - key, dcap);
+                        const float pe = fast_exp2(fmaf(x, c, -lse2));
                         bool ok = true;
-                        if constexpr (MASKED) ok = key >= lo && key <= hi && qin;
-                        const float p = ok ? fast_exp2(fmaf(x, c, -lse2)) : 0.f;
+                        if constexpr (MASKED) ok = (key >= lo) & (key <= hi) & qin;
+                        const float p = ok ? pe : 0.f;
                         ds2[i] = p * (dpacc[r + i] - dsum);
                         if constexpr (BIAS) ds2[i] *= dcap;
                     }
