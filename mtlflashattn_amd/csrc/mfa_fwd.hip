@@ -461,23 +461,9 @@ mfa_fwd16_kernel(KArgs a) {
     const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
     const int dq = Lk - Lq;
 
-    // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
-    for (int c = tid; c < BM * CPR; c += kThreads) {
-        const int row = c / CPR, col = (c % CPR) * 8;
-        u32x4_t val = {0, 0, 0, 0};
-        if (q0 + row < Lq && col < D)
-            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 2);
-        *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
-    }
-    __syncthreads();
     const int wq0 = q0 + wave * QB * 32;  // first query row of this wavefront
-    op_t qf[QB][DS];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-        for (int s = 0; s < DS; ++s)
-            qf[qb][s] = *reinterpret_cast<const op_t*>(smem + (wave * QB * 32 + qb * 32 + l32) * KST + 16 * s + 8 * half);
-    __syncthreads();
+    op_t qf[QB][DS];                       // Q as MFMA B operands (filled below)
+
 
     // ---- per-lane query state
     RowState rs[QB];
@@ -746,11 +732,30 @@ mfa_fwd16_kernel(KArgs a) {
         if constexpr (MFA_SETPRIO) __builtin_amdgcn_s_setprio(0);
     };
 
+    // the first K/V block's global loads run while Q is staged
+    if (nblk > 0) gload(jbeg);
+
+    // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
+    for (int c = tid; c < BM * CPR; c += kThreads) {
+        const int row = c / CPR, col = (c % CPR) * 8;
+        u32x4_t val = {0, 0, 0, 0};
+        if (q0 + row < Lq && col < D)
+            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 2);
+        *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int s = 0; s < DS; ++s)
+            qf[qb][s] = *reinterpret_cast<const op_t*>(smem + (wave * QB * 32 + qb * 32 + l32) * KST + 16 * s + 8 * half);
+    __syncthreads();
+
     // Block it is computed from LDS buffer it%2 while the registers hold
     // block it+1 (loaded during block it-1): its LDS stores and the global
     // loads of block it+2 are issued during block it, one barrier per block.
+    // (block 0's loads were issued before the Q tile was staged)
     if (nblk > 0) {
-        gload(jbeg);
         swrite(0);
         if (nblk > 1) gload(jbeg + BN);
         __syncthreads();
