@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MFA_ABI_VERSION 4
+#define MFA_ABI_VERSION 5
 
 /* element types (dtype_in / dtype_out) */
 #define MFA_DTYPE_F16 0
@@ -239,6 +239,10 @@ typedef struct mfa_bwd_params {
     int64_t dv_batch_stride, dv_seq_stride, dv_head_stride;
     int32_t dtype_grad; /* dtype of dq/dk/dv: dtype_in or MFA_DTYPE_F32 */
     int32_t reserved;
+    /* Optional gradient of the loss with respect to softmax_lse (fp32, same
+     * layout and strides as fwd.softmax_lse; NULL = zero).  Since
+     * d lse_i / d s_ij = P_ij, it enters as Dsum_i - dlse_i. */
+    const float* dlse;
 } mfa_bwd_params;
 
 /* 1 if mfa_bwd implements (dtype_in, head_dim): bf16/fp16, head_dim a

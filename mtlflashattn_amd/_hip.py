@@ -21,7 +21,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime first)
 
 from ._build import LIB_PATH
 
-MFA_ABI_VERSION = 4
+MFA_ABI_VERSION = 5
 MFA_DTYPE_F16 = 0
 MFA_DTYPE_BF16 = 1
 MFA_DTYPE_F32 = 2
@@ -75,7 +75,7 @@ class MfaBwdParams(ctypes.Structure):
         ("dq", _c_ptr), ("dq_batch_stride", _c_i64), ("dq_seq_stride", _c_i64), ("dq_head_stride", _c_i64),
         ("dk", _c_ptr), ("dk_batch_stride", _c_i64), ("dk_seq_stride", _c_i64), ("dk_head_stride", _c_i64),
         ("dv", _c_ptr), ("dv_batch_stride", _c_i64), ("dv_seq_stride", _c_i64), ("dv_head_stride", _c_i64),
-        ("dtype_grad", _c_i32), ("reserved", _c_i32),
+        ("dtype_grad", _c_i32), ("reserved", _c_i32), ("dlse", _c_ptr),
     ]
 
 

@@ -460,12 +460,13 @@ def _needs_grad(*tensors):
 
 
 def _run_bwd(q, k, v, out, dout, lse, *, scale, causal, softcap, window_left, window_right, alibi, alibi_bstride,
-             cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None, grad_f32=False):
+             cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None, grad_f32=False, dlse=None):
     """(dq, dk, dv) of the forward on [B, S, H, D] views (varlen: [1, T, H, D]).
 
     out: the forward's output in q.dtype; lse: its softmax_lse ([B, Hq, Lq]
-    dense, [Hq, T] varlen).  Returns new tensors shaped like q, k, v in
-    q.dtype (grad_f32=True: fp32, the parity mode).
+    dense, [Hq, T] varlen); dlse: optional gradient of lse (same shape).
+    Returns new tensors shaped like q, k, v in q.dtype (grad_f32=True: fp32,
+    the parity mode).
     """
     _kernel_mode()
     if q.dtype == torch.float32:
@@ -509,6 +510,9 @@ def _run_bwd(q, k, v, out, dout, lse, *, scale, causal, softcap, window_left, wi
     p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
     lse = lse.contiguous()
     p.softmax_lse = lse.data_ptr()
+    if dlse is not None:
+        dlse = dlse.to(device=q.device, dtype=torch.float32).contiguous()
+        bp.dlse = dlse.data_ptr()
     p.lse_batch_stride, p.lse_head_stride = (0, lse.stride(0)) if varlen else (lse.stride(0), lse.stride(1))
     bp.dout = do_.data_ptr()
     bp.do_batch_stride, bp.do_seq_stride, bp.do_head_stride = _strides_bsh(do_)
@@ -531,7 +535,7 @@ def _run_bwd(q, k, v, out, dout, lse, *, scale, causal, softcap, window_left, wi
 
 class _FlashAttnFn(torch.autograd.Function):
     """Heads-third dense attention with the HIP backward; returns (out, lse),
-    lse not differentiable."""
+    both differentiable (a gradient on lse enters the backward's row sums)."""
 
     @staticmethod
     def forward(ctx, q, k, v, scale, causal, softcap, window_left, window_right, alibi_slopes):
@@ -544,18 +548,21 @@ class _FlashAttnFn(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.cfg = dict(scale=scale, causal=causal, softcap=softcap, window_left=window_left,
                        window_right=window_right, alibi=alibi, alibi_bstride=bstride)
-        ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)
         return out, lse
 
     @staticmethod
-    def backward(ctx, dout, _dlse):
+    def backward(ctx, dout, dlse):
         q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = _run_bwd(q, k, v, out, dout, lse, **ctx.cfg)
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq, dk, dv = _run_bwd(q, k, v, out, dout, lse, dlse=dlse, **ctx.cfg)
         return dq, dk, dv, None, None, None, None, None, None
 
 
 class _FlashAttnVarlenFn(torch.autograd.Function):
-    """Packed varlen attention with the HIP backward; returns (out, lse [Hq, T])."""
+    """Packed varlen attention with the HIP backward; returns (out, lse [Hq, T]),
+    both differentiable."""
 
     @staticmethod
     def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left, window_right,
@@ -570,14 +577,16 @@ class _FlashAttnVarlenFn(torch.autograd.Function):
         ctx.cfg = dict(scale=scale, causal=causal, softcap=softcap, window_left=window_left,
                        window_right=window_right, alibi=alibi, alibi_bstride=bstride, seqlen_q=max_q,
                        seqlen_k=max_k)
-        ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)
         return out, lse
 
     @staticmethod
-    def backward(ctx, dout, _dlse):
+    def backward(ctx, dout, dlse):
         q, k, v, out, lse, cu_q, cu_k = ctx.saved_tensors
+        if dout is None:
+            dout = torch.zeros_like(out)
         dq, dk, dv = _run_bwd(q[None], k[None], v[None], out[None], dout[None], lse, cu_q=cu_q, cu_k=cu_k,
-                              **ctx.cfg)
+                              dlse=dlse, **ctx.cfg)
         return dq[0], dk[0], dv[0], None, None, None, None, None, None, None, None, None, None
 
 

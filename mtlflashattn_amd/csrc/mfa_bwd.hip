@@ -51,7 +51,8 @@ struct BArgs {
     int64_t dkb, dks, dkh;
     char* dv;
     int64_t dvb, dvs, dvh;
-    float* dsum;       // [B*Hq][Lq] rowsum(dO * O)
+    float* dsum;       // [B*Hq][Lq] rowsum(dO * O) - dlse
+    const float* dlse; // gradient of lse (softmax_lse layout), or NULL
     int32_t grad_f32;  // dq/dk/dv written as fp32
     int32_t T;         // tiles per unit (dsum: 16-row groups; dK/dV: key tiles; dQ: query tiles)
     int32_t Ukv;       // (sequence, K/V head) units = B * Hkv
@@ -219,7 +220,13 @@ __global__ void __launch_bounds__(kBThreads) mfa_bwd_dsum_kernel(BArgs a) {
     acc += __shfl_xor(acc, 4);
     acc += __shfl_xor(acc, 2);
     acc += __shfl_xor(acc, 1);
-    if (sub == 0 && row < qv.Lq) qv.dsum[row] = acc;
+    if (sub == 0 && row < qv.Lq) {
+        if (a.dlse) {  // d lse / d s = P: enters as Dsum - dlse (same offset as the lse row)
+            const float* dl = a.dlse + (qv.lse - a.f.lse);
+            acc -= dl[row];
+        }
+        qv.dsum[row] = acc;
+    }
 }
 
 // Store rows of a transposed accumulator (lane = row `idx` of the output,
@@ -772,6 +779,7 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     a.dv = static_cast<char*>(bp->dv);
     a.dvb = bp->dv_batch_stride; a.dvs = bp->dv_seq_stride; a.dvh = bp->dv_head_stride;
     a.grad_f32 = bp->dtype_grad == MFA_DTYPE_F32 ? 1 : 0;
+    a.dlse = bp->dlse;
     a.Ukv = p->batch * p->heads_kv;
     const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
     plan->ws_bytes = plan->empty ? 0 : ((rows * 4 + 255) / 256) * 256;

@@ -171,9 +171,10 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=No
 
 
 def attention_grads(q, k, v, dout, softmax_scale=None, causal=False, window_size=(-1, -1), softcap=0.0,
-                    alibi_slopes=None, dtype=torch.float32):
-    """Gradients (dq, dk, dv) of sum(out * dout) for heads-third q [B,Lq,Hq,D],
-    k/v [B,Lk,Hkv,D], by torch autograd through flash_torch (CPU, `dtype`).
+                    alibi_slopes=None, dtype=torch.float32, dlse=None):
+    """Gradients (dq, dk, dv) of sum(out * dout) (+ sum(lse * dlse) when dlse,
+    [B,Hq,Lq], is given) for heads-third q [B,Lq,Hq,D], k/v [B,Lk,Hkv,D], by
+    torch autograd through flash_torch (CPU, `dtype`).
 
     The reference has no backward (metal_flash_attn/__init__.py:3-4); these
     are the exact gradients of its forward math (_kernel.py:1165-1208), GQA
@@ -184,9 +185,14 @@ def attention_grads(q, k, v, dout, softmax_scale=None, causal=False, window_size
     alibi = broadcast_alibi(alibi_slopes, B, Hq) if alibi_slopes is not None else None
     qd, kd, vd = (t.detach().cpu().to(dtype).requires_grad_(True) for t in (q, k, v))
     with torch.enable_grad():
-        out = flash_torch(qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), scale, causal, softcap,
-                          window_size[0], window_size[1], alibi, grad=True, dtype=dtype)
-        (out * dout.detach().cpu().to(dtype).transpose(1, 2)).sum().backward()
+        out, lse = flash_torch(qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), scale, causal, softcap,
+                               window_size[0], window_size[1], alibi, grad=True, dtype=dtype, return_lse=True)
+        loss = (out * dout.detach().cpu().to(dtype).transpose(1, 2)).sum()
+        if dlse is not None:
+            # rows without a valid key have lse = -inf and no gradient
+            ld = dlse.detach().cpu().to(dtype)
+            loss = loss + torch.where(torch.isinf(lse), torch.zeros_like(lse), lse * ld).sum()
+        loss.backward()
     return qd.grad, kd.grad, vd.grad
 
 

@@ -197,3 +197,29 @@ def test_gqa_grads_equal_summed_repeated_heads():
     for g, r in ((dk, dk_r), (dv, dv_r)):
         summed = r.float().reshape(1, 170, 2, 4, 64).sum(3)
         assert rel_err(g, summed.cpu()) <= GRAD_REL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+def test_lse_gradient(dtype):
+    # loss = sum(out * dout) + sum(lse * dlse): the lse gradient enters as Dsum - dlse
+    q, k, v = make_qkv(1, 160, 220, 4, 2, 64, dtype, seed=15)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(15)).to(DEV, dtype)
+    dlse = torch.randn(1, 4, 160, generator=torch.Generator().manual_seed(16)).to(DEV)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    out, lse = mfa.flash_attn_func_with_lse(qg, kg, vg, causal=True)
+    ((out.float() * dout.float()).sum() + (lse * dlse).sum()).backward()
+    ref = chunked.attention_grads(q, k, v, dout, causal=True, dlse=dlse)
+    check_grads((qg.grad, kg.grad, vg.grad), ref, dtype, "lse gradient", factor=2.0)
+
+
+def test_merged_key_shards_train_like_full_attention():
+    # context-parallel use: attention over key shards merged by lse, end to end
+    # differentiable, gives the gradients of attention over all keys
+    q, k, v = make_qkv(1, 120, 300, 4, 4, 64, torch.bfloat16, seed=17)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(17)).to(DEV, torch.bfloat16)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    parts = [mfa.flash_attn_func_with_lse(qg, kg[:, a:b], vg[:, a:b]) for a, b in ((0, 100), (100, 101), (101, 300))]
+    out, _ = mfa.merge_attention_partials([o for o, _ in parts], [l for _, l in parts])
+    (out.float() * dout.float()).sum().backward()
+    ref = chunked.attention_grads(q, k, v, dout)
+    check_grads((qg.grad, kg.grad, vg.grad), ref, torch.bfloat16, "merged shards", factor=2.0)

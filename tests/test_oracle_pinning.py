@@ -476,3 +476,24 @@ def test_fp32_gradients_agree_with_float64():
     g64 = chunked.attention_grads(*args, causal=True, softcap=5.0, dtype=torch.float64)
     for a, b in zip(g32, g64):
         close(a, b, atol=2e-5)
+
+
+def test_lse_gradient_matches_finite_differences_and_closed_form():
+    g = torch.Generator().manual_seed(27)
+    q = torch.randn(1, 5, 2, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 7, 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(1, 7, 2, 8, generator=g, dtype=torch.float64)
+
+    def lse_of(q, k):
+        return chunked.flash_torch(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), 0.4, True, grad=True,
+                                   dtype=torch.float64, return_lse=True)[1]
+
+    assert torch.autograd.gradcheck(lse_of, (q.clone().requires_grad_(True), k.clone().requires_grad_(True)))
+    # d lse_i / d q_i = scale * sum_j P_ij k_j (P the row's softmax): with dout = 0, dlse = 1
+    dq, _, _ = chunked.attention_grads(q, k, v, torch.zeros_like(q), softmax_scale=0.4, causal=True,
+                                       dlse=torch.ones(1, 2, 5, dtype=torch.float64), dtype=torch.float64)
+    s = torch.einsum("bihd,bjhd->bhij", q, k) * 0.4
+    mask = torch.arange(7)[None, :] > (torch.arange(5)[:, None] + 2)
+    p = torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1)
+    want = 0.4 * torch.einsum("bhij,bjhd->bihd", p, k)
+    close(dq, want, atol=1e-10)
