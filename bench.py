@@ -47,7 +47,7 @@ def measured_traffic(cfg: int):
     import glob
     import re
 
-    for path in sorted(glob.glob(os.path.join(REPO, "profiles", f"*_cfg{cfg}.md"))):
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", f"mfa_fwd*_cfg{cfg}.md"))):
         m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", open(path).read(), re.M)
         if m:
             return int(m.group(1))
