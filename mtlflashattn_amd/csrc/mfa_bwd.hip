@@ -56,6 +56,13 @@ struct BArgs {
     int32_t grad_f32;  // dq/dk/dv written as fp32
     int32_t T;         // tiles per unit (dsum: 16-row groups; dK/dV: key tiles; dQ: query tiles)
     int32_t Ukv;       // (sequence, K/V head) units = B * Hkv
+    // grouped-query heads split over dK/dV workgroups: G groups of R/G query
+    // heads each; G > 1 writes fp32 partials ws_dk/ws_dv [G][B*Hkv][Lk][DP]
+    // that mfa_bwd_dkdv_sum_kernel adds in group order
+    int32_t G;
+    int32_t ws_ld;  // DP
+    float* ws_dk;
+    float* ws_dv;
 };
 
 // Per (sequence, query head): q, o, dO, dq, lse and Dsum rows.
@@ -277,7 +284,8 @@ mfa_bwd_dkdv_kernel(BArgs a) {
 
     const KArgs& f = a.f;
     const int bid = blockIdx.x;
-    const int ktile = bid / a.Ukv, unit = bid - ktile * a.Ukv;
+    const int ktile = bid / (a.Ukv * a.G), rem = bid - ktile * (a.Ukv * a.G);
+    const int unit = rem / a.G, grp = rem - unit * a.G;
     const int b = unit / f.Hkv, hkv = unit - b * f.Hkv;
     const KView kv = k_view(a, b, hkv);
     const int Lk = kv.Lk, D = f.D;
@@ -310,7 +318,8 @@ mfa_bwd_dkdv_kernel(BArgs a) {
 
     // Query blocks: every head of the K/V group, the blocks whose rows can
     // see [k0, k1] (the same range for every head: lengths are per sequence).
-    const int R = f.Hq / f.Hkv;
+    const int R = f.Hq / f.Hkv / a.G;       // query heads of this workgroup
+    const int hq0 = hkv * R * a.G + grp * R;  // the first of them
     const int Lq = f.cu_q ? f.cu_q[b + 1] - f.cu_q[b] : f.Lq;
     const int dq = Lk - Lq;
     int qlo = 0, qhi = Lq - 1;
@@ -340,7 +349,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     auto gload = [&](int step) {
         const int rr = step / nqb;
         const int q0 = qb0 + (step - rr * nqb) * BQ;
-        const QView qv = q_view(a, b, hkv * R + rr);
+        const QView qv = q_view(a, b, hq0 + rr);
         const int rm1 = min(Lq - q0, BQ) - 1;  // q0 < Lq
         const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(qv.q + (int64_t)q0 * f.qs * 2), (short)0, (int)(((int64_t)rm1 * f.qs + D) * 2), kBufferDword3);
@@ -380,7 +389,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         if (step + 1 < nsteps) gload(step + 1);  // in flight during this step's MFMAs
         const int rr = step / nqb;
         const int q0 = qb0 + (step - rr * nqb) * BQ;
-        const int hq = hkv * R + rr;
+        const int hq = hq0 + rr;
         const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
         {
             const uint16_t* qsb = q_s[buf];
@@ -457,10 +466,55 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         __syncthreads();
     }
     if (key < Lk) {
-        const bool f32o = a.grad_f32 != 0;
-        const int ges = f32o ? 4 : 2;
-        store_rows<DB>(kv.dk + (int64_t)key * a.dks * ges, 0, D, f32o, IS_BF16, dka, f.scale, half);
-        store_rows<DB>(kv.dv + (int64_t)key * a.dvs * ges, 0, D, f32o, IS_BF16, dva, 1.f, half);
+        if (a.G > 1) {  // this group's partial sums, unscaled, fp32
+            const int64_t row = ((int64_t)grp * a.Ukv + unit) * f.Lk + key;
+            store_rows<DB>(reinterpret_cast<char*>(a.ws_dk + row * a.ws_ld), 0, D, true, IS_BF16, dka, 1.f, half);
+            store_rows<DB>(reinterpret_cast<char*>(a.ws_dv + row * a.ws_ld), 0, D, true, IS_BF16, dva, 1.f, half);
+        } else {
+            const bool f32o = a.grad_f32 != 0;
+            const int ges = f32o ? 4 : 2;
+            store_rows<DB>(kv.dk + (int64_t)key * a.dks * ges, 0, D, f32o, IS_BF16, dka, f.scale, half);
+            store_rows<DB>(kv.dv + (int64_t)key * a.dvs * ges, 0, D, f32o, IS_BF16, dva, 1.f, half);
+        }
+    }
+}
+
+// Sum of the G head-group partials of dK / dV in group order (deterministic),
+// scaled (dK) and stored in the gradient dtype: 4 elements per thread.
+template <bool IS_BF16>
+__global__ void __launch_bounds__(kBThreads) mfa_bwd_dkdv_sum_kernel(BArgs a) {
+    const KArgs& f = a.f;
+    const int per_row = f.D / 4;
+    const int64_t idx = (int64_t)blockIdx.x * kBThreads + threadIdx.x;
+    const int64_t rows = (int64_t)a.Ukv * f.Lk;
+    if (idx >= rows * per_row) return;
+    const int64_t r = idx / per_row;
+    const int d = (int)(idx - r * per_row) * 4;
+    const int unit = (int)(r / f.Lk), key = (int)(r - (int64_t)unit * f.Lk);
+    const int b = unit / f.Hkv, hkv = unit - b * f.Hkv;
+    const KView kv = k_view(a, b, hkv);
+    if (key >= kv.Lk) return;
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+    for (int g = 0; g < a.G; ++g) {
+        const int64_t off = (((int64_t)g * a.Ukv + unit) * f.Lk + key) * a.ws_ld + d;
+        const float4 x = *reinterpret_cast<const float4*>(a.ws_dk + off);
+        const float4 y = *reinterpret_cast<const float4*>(a.ws_dv + off);
+        sk.x += x.x; sk.y += x.y; sk.z += x.z; sk.w += x.w;
+        sv.x += y.x; sv.y += y.y; sv.z += y.z; sv.w += y.w;
+    }
+    const float sc = f.scale;
+    const float k4[4] = {sk.x * sc, sk.y * sc, sk.z * sc, sk.w * sc};
+    const float v4[4] = {sv.x, sv.y, sv.z, sv.w};
+    if (a.grad_f32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(kv.dk) + (int64_t)key * a.dks + d) =
+            make_float4(k4[0], k4[1], k4[2], k4[3]);
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(kv.dv) + (int64_t)key * a.dvs + d) =
+            make_float4(v4[0], v4[1], v4[2], v4[3]);
+    } else {
+        const uint32_t kw0 = Ops<IS_BF16>::pack(k4[0], k4[1]), kw1 = Ops<IS_BF16>::pack(k4[2], k4[3]);
+        const uint32_t vw0 = Ops<IS_BF16>::pack(v4[0], v4[1]), vw1 = Ops<IS_BF16>::pack(v4[2], v4[3]);
+        *reinterpret_cast<u32x2_t*>(kv.dk + ((int64_t)key * a.dks + d) * 2) = u32x2_t{kw0, kw1};
+        *reinterpret_cast<u32x2_t*>(kv.dv + ((int64_t)key * a.dvs + d) * 2) = u32x2_t{vw0, vw1};
     }
 }
 
@@ -652,13 +706,14 @@ int bset_err(int code, const char* fmt, ...) {
 typedef void (*bkernel_fn)(BArgs);
 
 struct BwdKernels {
-    bkernel_fn dsum, dkdv, dq;
+    bkernel_fn dsum, dkdv, dq, dkdv_sum;
 };
 
 template <int DP, bool IS_BF16>
 BwdKernels bwd_kernels(bool bias) {
     BwdKernels k;
     k.dsum = mfa_bwd_dsum_kernel<IS_BF16>;
+    k.dkdv_sum = mfa_bwd_dkdv_sum_kernel<IS_BF16>;
     k.dkdv = bias ? (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, true> : (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, false>;
     k.dq = bias ? (bkernel_fn)mfa_bwd_dq_kernel<DP, IS_BF16, true> : (bkernel_fn)mfa_bwd_dq_kernel<DP, IS_BF16, false>;
     return k;
@@ -678,7 +733,8 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 struct BPlan {
     BArgs a;
     BwdKernels k;
-    int grid_dsum, grid_dkdv, grid_dq;
+    int grid_dsum, grid_dkdv, grid_dq, grid_dkdv_sum;
+    int64_t dsum_bytes;  // workspace: row sums first, then the dK/dV partials
     int64_t ws_bytes;
     bool empty;
 };
@@ -782,15 +838,27 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     a.dlse = bp->dlse;
     a.Ukv = p->batch * p->heads_kv;
     const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
-    plan->ws_bytes = plan->empty ? 0 : ((rows * 4 + 255) / 256) * 256;
+    plan->dsum_bytes = ((rows * 4 + 255) / 256) * 256;
+    // Grouped-query heads: one dK/dV workgroup per query head (fp32 partials
+    // summed afterwards) when that workspace stays within 2 GiB; otherwise
+    // each workgroup loops over its K/V head's query heads.
+    const int R = p->heads_q / p->heads_kv;
+    const int64_t part = (int64_t)a.Ukv * p->seqlen_k * dp * 4;  // one group's dK (or dV) partials
+    a.G = (R > 1 && 2 * R * part <= ((int64_t)2 << 30)) ? R : 1;
+    a.ws_ld = dp;
+    const int64_t part_bytes = a.G > 1 ? 2 * a.G * part : 0;
+    plan->ws_bytes = plan->empty ? 0 : plan->dsum_bytes + part_bytes;
     const int64_t g1 = (int64_t)f.U * ((p->seqlen_q + 15) / 16);
-    const int64_t g2 = (int64_t)a.Ukv * ((p->seqlen_k + 127) / 128);
+    const int64_t g2 = (int64_t)a.Ukv * a.G * ((p->seqlen_k + 127) / 128);
     const int64_t g3 = (int64_t)f.U * ((p->seqlen_q + 127) / 128);
     if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL)
         return bset_err(MFA_ERR_INVALID, "mfa_bwd: problem too large");
     plan->grid_dsum = (int)g1;
     plan->grid_dkdv = (int)g2;
     plan->grid_dq = (int)g3;
+    const int64_t g4 = ((int64_t)a.Ukv * p->seqlen_k * (D / 4) + kBThreads - 1) / kBThreads;
+    if (g4 > 0x7fffffffLL) return bset_err(MFA_ERR_INVALID, "mfa_bwd: problem too large");
+    plan->grid_dkdv_sum = (int)g4;
     return MFA_OK;
 }
 
@@ -826,11 +894,16 @@ int mfa_bwd(const mfa_bwd_params* params, void* workspace, int64_t workspace_byt
                         (long long)plan.ws_bytes);
     BArgs& a = plan.a;
     a.dsum = static_cast<float*>(workspace);
+    if (a.G > 1) {
+        a.ws_dk = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.dsum_bytes);
+        a.ws_dv = a.ws_dk + (int64_t)a.G * a.Ukv * params->fwd.seqlen_k * a.ws_ld;
+    }
     const hipStream_t st = static_cast<hipStream_t>(stream);
     a.T = (params->fwd.seqlen_q + 15) / 16;
     hipLaunchKernelGGL(plan.k.dsum, dim3(plan.grid_dsum), dim3(kBThreads), 0, st, a);
     a.T = (params->fwd.seqlen_k + 127) / 128;
     hipLaunchKernelGGL(plan.k.dkdv, dim3(plan.grid_dkdv), dim3(kBThreads), 0, st, a);
+    if (a.G > 1) hipLaunchKernelGGL(plan.k.dkdv_sum, dim3(plan.grid_dkdv_sum), dim3(kBThreads), 0, st, a);
     a.T = (params->fwd.seqlen_q + 127) / 128;
     hipLaunchKernelGGL(plan.k.dq, dim3(plan.grid_dq), dim3(kBThreads), 0, st, a);
     const hipError_t e = hipGetLastError();
