@@ -248,8 +248,11 @@ typedef struct mfa_bwd_params {
 /* 1 if mfa_bwd implements (dtype_in, head_dim): bf16/fp16, head_dim a
  * multiple of 8 up to MFA_MAX_HEAD_DIM. */
 int mfa_bwd_supported(int32_t dtype_in, int32_t head_dim);
-/* Device workspace mfa_bwd needs (the fp32 row sums Dsum), 0 for an empty
- * problem, < 0 on error. */
+/* Device workspace mfa_bwd needs, 0 for an empty problem, < 0 on error: the
+ * fp32 row sums Dsum, and with grouped-query heads (heads_q > heads_kv) the
+ * fp32 dK/dV partials of each query head (2 * heads_q * batch * seqlen_k *
+ * padded head_dim * 4 bytes) when they fit in 2 GiB -- the query heads of a
+ * K/V head then run in parallel workgroups and are summed in head order. */
 int64_t mfa_bwd_workspace_bytes(const mfa_bwd_params* params);
 /* Enqueue the backward kernels on `stream`; `workspace`: 256-byte aligned
  * device buffer of at least mfa_bwd_workspace_bytes bytes, owned by the
