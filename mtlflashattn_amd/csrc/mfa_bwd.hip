@@ -817,6 +817,7 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     f.scale_log2 = p->scale * kLog2e;
     f.softcap = p->softcap;
     f.softcap_k = p->softcap > 0.f ? 2.f * kLog2e / p->softcap : 0.f;
+    f.softcap_sk = p->scale * f.softcap_k;
     const int64_t wmax = (int64_t)p->seqlen_q + (int64_t)p->seqlen_k + 1;
     f.wl = p->window_left < 0 ? -1 : (int32_t)(p->window_left > wmax ? wmax : p->window_left);
     f.wr = p->window_right < 0 ? -1 : (int32_t)(p->window_right > wmax ? wmax : p->window_right);

@@ -49,6 +49,7 @@ struct KArgs {
     float scale_log2; // scale * log2(e)
     float softcap;    // 0 = off
     float softcap_k;  // 2 * log2(e) / softcap
+    float softcap_sk; // scale * softcap_k (the soft-cap of a raw score in one exponent)
     int32_t wl, wr, causal;
     int32_t out_f32;
     // schedule

@@ -123,20 +123,22 @@ __device__ __forceinline__ void qb_transform(const KArgs& a, f32x16_t (&s)[NKB],
                                              int half) {
     if constexpr (BIAS) {
         // natural-log units: x = scale*s, soft-cap, ALiBi (_kernel.py:75-77)
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[kb][r] *= a.scale;
         if (a.softcap > 0.f) {
-            // c * tanh(x / c) = c - 2c / (exp(2x/c) + 1)
+            // c * tanh(x / c) = c - 2c / (exp(2x/c) + 1), the scale folded
+            // into the exponent's constant (x itself is not needed)
             const float c2 = -2.f * a.softcap;
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float e = fast_exp2(s[kb][r] * a.softcap_k);
+                    const float e = fast_exp2(s[kb][r] * a.softcap_sk);
                     s[kb][r] = fmaf(c2, __builtin_amdgcn_rcpf(e + 1.f), a.softcap);
                 }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[kb][r] *= a.scale;
         }
         if (a.alibi) {
 #pragma unroll
@@ -1589,6 +1591,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     a.scale_log2 = p->scale * kLog2e;
     a.softcap = p->softcap;
     a.softcap_k = p->softcap > 0.f ? 2.f * kLog2e / p->softcap : 0.f;
+    a.softcap_sk = p->scale * a.softcap_k;
     // clamp windows so center +/- window cannot overflow int32
     const int64_t wmax = (int64_t)p->seqlen_q + (int64_t)p->seqlen_k + 1;
     a.wl = p->window_left < 0 ? -1 : (int32_t)(p->window_left > wmax ? wmax : p->window_left);
