@@ -223,3 +223,46 @@ def test_merged_key_shards_train_like_full_attention():
     (out.float() * dout.float()).sum().backward()
     ref = chunked.attention_grads(q, k, v, dout)
     check_grads((qg.grad, kg.grad, vg.grad), ref, torch.bfloat16, "merged shards", factor=2.0)
+
+
+@pytest.mark.parametrize("lq,lk,causal", [(5, 1, False), (1, 1, True), (1, 700, True), (3, 2, True), (33, 65, False),
+                                          (200, 7, True)])
+def test_edge_lengths(lq, lk, causal):
+    q, k, v = make_qkv(2, lq, lk, 4, 2, 64, torch.bfloat16, seed=lq * 100 + lk)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(lq + lk)).to(DEV, torch.bfloat16)
+    _, *got = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=causal), q, k, v, dout)
+    ref = chunked.attention_grads(q, k, v, dout, causal=causal)
+    for name, g, r in zip(("dq", "dk", "dv"), got, ref):
+        if r.abs().max() == 0:
+            # identically zero in exact arithmetic (one key: dS = dP - Dsum = 0);
+            # the kernel's two fp32 sums of dO.v differ only in rounding
+            assert g.float().abs().max().item() <= 1e-3, f"{name} Lq={lq} Lk={lk}"
+        else:
+            e = rel_err(g, r)
+            assert e <= 2 * GRAD_REL[torch.bfloat16], f"{name} Lq={lq} Lk={lk} causal={causal}: rel err {e:.2e}"
+
+
+def test_varlen_with_empty_key_sequences_and_lse_gradient():
+    lens_q, lens_k = [3, 4, 0, 2], [0, 50, 9, 300]
+    q, k, v, cu_q, cu_k = make_varlen(lens_q, lens_k, 4, 4, 64, torch.float16, seed=18)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(18)).to(DEV, torch.float16)
+    dlse = torch.randn(4, sum(lens_q), generator=torch.Generator().manual_seed(19)).to(DEV)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    out, lse = mfa.flash_attn_varlen_func_with_lse(qg, kg, vg, cu_q, cu_k, max(lens_q), max(lens_k), causal=True)
+    assert torch.isneginf(lse[:, :3]).all()  # the first sequence has no key
+    ((out.float() * dout.float()).sum() + (torch.where(torch.isinf(lse), 0, lse) * dlse).sum()).backward()
+    sq = [0] + torch.tensor(lens_q).cumsum(0).tolist()
+    sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()
+    ref = chunked.attention_grads_varlen(q, k, v, dout, cu_q.cpu(), cu_k.cpu(), causal=True)
+    # the lse term per sequence through the dense oracle
+    for i in range(len(lens_q)):
+        a, b, c, d = sq[i], sq[i + 1], sk[i], sk[i + 1]
+        if b == a or d == c:
+            continue
+        gi = chunked.attention_grads(q[None, a:b], k[None, c:d], v[None, c:d], torch.zeros_like(dout[None, a:b]),
+                                     causal=True, dlse=dlse[None, :, a:b])
+        ref[0][a:b] += gi[0][0]
+        ref[1][c:d] += gi[1][0]
+        ref[2][c:d] += gi[2][0]
+    check_grads((qg.grad, kg.grad, vg.grad), ref, torch.float16, "varlen + lse gradient", factor=2.0)
+    assert torch.count_nonzero(qg.grad[:3]) == 0
