@@ -117,6 +117,19 @@ def make_config(cfg: int):
                     algo=4 * pairs * D, varlen=None, hbm_bytes=2 * (2 * B * Lq * H * D + 2 * B * Lk * H * D),
                     workload=f"cfg{cfg} (HBM-bound, not a BASELINE config): bf16 B={B} Lq={Lq} Lk={Lk} "
                              f"H={H} D={D} non-causal, seed {cfg}")
+    if cfg == 9:
+        # not a BASELINE config: single-row grouped-query decode (query heads
+        # of a K/V head computed together; HBM-bound, roofline in GB/s)
+        g = torch.Generator().manual_seed(9)
+        B, Lk, Hq, Hkv, D = 64, 4096, 32, 8, 128
+        q = torch.randn(B, 1, Hq, D, generator=g).to(dev, torch.bfloat16)
+        k = torch.randn(B, Lk, Hkv, D, generator=g).to(dev, torch.bfloat16)
+        v = torch.randn(B, Lk, Hkv, D, generator=g).to(dev, torch.bfloat16)
+        pairs = B * Hq * Lk
+        return dict(q=q, k=k, v=v, kw=dict(causal=True), dtype="bf16", D=D, formula=4 * pairs * D,
+                    algo=4 * pairs * D, varlen=None, hbm_bytes=2 * (2 * B * Hq * D + 2 * B * Lk * Hkv * D),
+                    workload=f"cfg9 (HBM-bound, not a BASELINE config): bf16 B={B} Lq=1 Lk={Lk} Hq={Hq} Hkv={Hkv} "
+                             f"D={D} causal (grouped-query decode), seed 9")
     raise SystemExit(f"unknown config {cfg}")
 
 
@@ -219,9 +232,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8],
-                    help="BASELINE config 2-5 (default 2, the headline); 6-8 are HBM-bound short-L "
-                         "shapes (roofline in GB/s; 8 runs split-KV)")
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8, 9],
+                    help="BASELINE config 2-5 (default 2, the headline); 6-9 are HBM-bound short-L / decode "
+                         "shapes (roofline in GB/s; 8 runs split-KV, 9 is grouped-query decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--backward", action="store_true",
                     help="time the HIP backward (dq, dk, dv) of the config instead of the forward (configs 2-5; "

@@ -51,6 +51,7 @@ struct KArgs {
     float softcap_k;  // 2 * log2(e) / softcap
     float softcap_sk; // scale * softcap_k (the soft-cap of a raw score in one exponent)
     int32_t wl, wr, causal;
+    int32_t decode_pack;  // rows are the query heads of one K/V head (single-row GQA decode)
     int32_t out_f32;
     // schedule
     int32_t T;        // query tiles per (sequence, head)

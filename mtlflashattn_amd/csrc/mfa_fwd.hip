@@ -183,13 +183,16 @@ __device__ __forceinline__ float qb_max(const f32x16_t (&s)[NKB]) {
 
 // Running-max update from the block max mx.  The reference max of the wave
 // moves (to every row's exact max) only when some row's max grew by more than
-// MFA_RESCALE_TAU in the exp2 domain; otherwise probabilities are taken
-// against the previous reference, so p <= 2^TAU.  O and l always use the same
+// tau (MFA_RESCALE_TAU) in the exp2 domain; otherwise probabilities are taken
+// against the previous reference, so p <= 2^tau.  O and l always use the same
 // reference, so the final O/l is unaffected.  Returns true when the reference
 // moved (wave-uniform); alpha is then the factor for O and l.  Rows with no
 // valid key so far keep m = -inf and get mu = 0, so masked scores give p = 0.
-__device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float& mu, float& alpha) {
-    const bool moved = __any((mx - rs.m) * c > (float)MFA_RESCALE_TAU);
+// With tau = 0 a row whose max did not grow gets alpha = exp2(0) = 1 exactly,
+// so each row's arithmetic is independent of the other rows of its wave.
+__device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float& mu, float& alpha,
+                                          float tau = (float)MFA_RESCALE_TAU) {
+    const bool moved = __any((mx - rs.m) * c > tau);
     alpha = 1.f;
     if (moved) {
         const float mn = fmaxf(rs.m, mx);
@@ -205,8 +208,9 @@ __device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float
 // to the caller, by `alpha`, exactly when it returns true.  (alpha is not
 // forced to 1 otherwise, so the caller's conditional rescale cannot be
 // turned into an unconditional multiply by 1.)
-__device__ __forceinline__ bool qb_update_flat(RowState& rs, float mx, float c, float& mu, float& alpha) {
-    const bool moved = __any((mx - rs.m) * c > (float)MFA_RESCALE_TAU);
+__device__ __forceinline__ bool qb_update_flat(RowState& rs, float mx, float c, float& mu, float& alpha,
+                                               float tau = (float)MFA_RESCALE_TAU) {
+    const bool moved = __any((mx - rs.m) * c > tau);
     const float mn = fmaxf(rs.m, mx);
     alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
     rs.m = moved ? mn : rs.m;
@@ -486,6 +490,10 @@ mfa_fwd16_kernel(KArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.f;
     const float c = BIAS ? kLog2e : a.scale_log2;
+    // exact (per-row) rescales for single-row sequences and packed
+    // grouped-query decode rows: their results do not depend on which rows
+    // share a wave, so packed heads equal unpacked ones bit for bit
+    const float tau = (Lq == 1 || a.decode_pack) ? 0.f : (float)MFA_RESCALE_TAU;
 
     // ---- key range of the workgroup and of this wavefront
     const int qlast = min(q0 + BM, Lq) - 1;
@@ -612,7 +620,7 @@ mfa_fwd16_kernel(KArgs a) {
         for (int qb = 0; qb < QB; ++qb) {
             qb_transform<NKB, BIAS, MASKED>(a, sacc[qb], rs[qb], j, half);
             float mu, alpha;
-            if (qb_update(rs[qb], qb_max<NKB>(sacc[qb]), c, mu, alpha)) scale_rows<DB>(o[qb], alpha);
+            if (qb_update(rs[qb], qb_max<NKB>(sacc[qb]), c, mu, alpha, tau)) scale_rows<DB>(o[qb], alpha);
             qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu, c);
         }
 #pragma unroll
@@ -701,7 +709,7 @@ mfa_fwd16_kernel(KArgs a) {
                         mpart[1] = fmaxf(mpart[1], sacc[qb][ci][r + 1]);
                     }
                 } else if (ci == NKB) {  // merge halves, new running max
-                    moved = qb_update(rs[qb], max_halves(fmaxf(mpart[0], mpart[1])), c, mu, alpha);
+                    moved = qb_update(rs[qb], max_halves(fmaxf(mpart[0], mpart[1])), c, mu, alpha, tau);
                     lacc[0] = rs[qb].l;
                 } else if (ci < NKB + 1 + DB) {  // rescale O rows (only if some row's max moved)
                     const int db = ci - NKB - 1;
@@ -913,6 +921,9 @@ mfa_fwd16_pp_kernel(KArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.f;
     const float c = BIAS ? kLog2e : a.scale_log2;
+    // per-row rescales for single-row sequences, as in the 4-wavefront kernel
+    // (the two kernels then agree bit for bit on every shape)
+    const float tau = Lq == 1 ? 0.f : (float)MFA_RESCALE_TAU;
 
     // ---- key range of the workgroup
     const int qlast = min(q0 + BM, Lq) - 1;
@@ -1114,7 +1125,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) mx[qb] = qb_max<NKB>(sacc[qb]);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_update_flat(rs[qb], mx[qb], c, mu[qb], alpha[qb]);
+        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_update_flat(rs[qb], mx[qb], c, mu[qb], alpha[qb], tau);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu[qb], c);
 #pragma unroll
@@ -1468,6 +1479,30 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     if (!p) return set_err(MFA_ERR_INVALID, "mfa_fwd: params is NULL");
+    // Single-row grouped-query decode: the R query heads of a K/V head become
+    // the R rows of one sequence (the same q/o memory through other strides),
+    // so one workgroup reads each K/V head once for all of them.  Exact for
+    // rows whose valid keys do not depend on their position -- no window, no
+    // ALiBi; causal with one query row admits every key -- and, with the
+    // per-row rescales of such rows, bit-identical to the unpacked call.
+    mfa_fwd_params packed;
+    bool pack = false;
+    if (p->dtype_in != MFA_DTYPE_F32 && !p->cu_seqlens_q && p->seqlen_q == 1 && p->heads_kv > 0 &&
+        p->heads_q > p->heads_kv && p->heads_q % p->heads_kv == 0 && p->window_left < 0 && p->window_right < 0 &&
+        !p->alibi_slopes && (!p->softmax_lse || p->lse_head_stride == 1) && p->tile_hint != MFA_TILE_PINGPONG) {
+        const int R = p->heads_q / p->heads_kv;
+        packed = *p;
+        packed.seqlen_q = R;
+        packed.heads_q = p->heads_kv;
+        packed.q_seq_stride = p->q_head_stride;
+        packed.q_head_stride = p->q_head_stride * R;
+        packed.o_seq_stride = p->o_head_stride;
+        packed.o_head_stride = p->o_head_stride * R;
+        packed.causal = 0;
+        if (p->softmax_lse) packed.lse_head_stride = R;
+        p = &packed;
+        pack = true;
+    }
     const int din = p->dtype_in, dout = p->dtype_out;
     if (din != MFA_DTYPE_F16 && din != MFA_DTYPE_BF16 && din != MFA_DTYPE_F32)
         return set_err(MFA_ERR_INVALID, "mfa_fwd: unknown dtype_in %d", din);
@@ -1597,6 +1632,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     a.wl = p->window_left < 0 ? -1 : (int32_t)(p->window_left > wmax ? wmax : p->window_left);
     a.wr = p->window_right < 0 ? -1 : (int32_t)(p->window_right > wmax ? wmax : p->window_right);
     a.causal = p->causal ? 1 : 0;
+    a.decode_pack = pack ? 1 : 0;
     a.out_f32 = dout == MFA_DTYPE_F32 ? 1 : 0;
     a.lse = p->softmax_lse;
     a.lse_b = p->lse_batch_stride;
@@ -1734,14 +1770,16 @@ int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* work
         return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: workspace of %lld bytes, %lld needed",
                        (long long)workspace_bytes, (long long)plan.ws_bytes);
     KArgs& a = plan.args;
-    const int64_t rows = (int64_t)a.nsplit * a.U * params->seqlen_q;
+    // (the planned rows: a packed grouped-query decode has a.Lq = query heads
+    // per K/V head rows per unit, not the caller's seqlen_q)
+    const int64_t rows = (int64_t)a.nsplit * a.U * a.Lq;
     a.ws_o = static_cast<float*>(workspace);
     a.ws_lse = a.ws_o + rows * a.ws_ld;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     // one chunk (every key range fits): the kernel stores O itself
     hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, st, a);
     if (a.nsplit > 1)
-        hipLaunchKernelGGL(plan.combine, dim3((unsigned)((int64_t)a.U * params->seqlen_q)), dim3(64), 0, st, a);
+        hipLaunchKernelGGL(plan.combine, dim3((unsigned)((int64_t)a.U * a.Lq)), dim3(64), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd_splitkv: launch failed: %s", hipGetErrorString(e));
     return MFA_OK;
