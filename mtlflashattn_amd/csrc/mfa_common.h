@@ -52,6 +52,11 @@ struct KArgs {
     float softcap_sk; // scale * softcap_k (the soft-cap of a raw score in one exponent)
     int32_t wl, wr, causal;
     int32_t decode_pack;  // rows are the query heads of one K/V head (single-row GQA decode)
+    // varlen: element strides between the tokens of q / o at which sequences
+    // start, and query rows per token (pack_r = query heads per K/V head when
+    // packed, else 1; rows then step by qs / os)
+    int64_t qts, ots;
+    int32_t pack_r;
     int32_t out_f32;
     // schedule
     int32_t T;        // query tiles per (sequence, head)
@@ -215,14 +220,14 @@ __device__ __forceinline__ SeqView seq_view(const KArgs& a, int b, int hq) {
     if (a.cu_q) {
         const int q_start = a.cu_q[b];
         const int k_start = a.cu_k[b];
-        s.Lq = a.cu_q[b + 1] - q_start;
+        s.Lq = (a.cu_q[b + 1] - q_start) * a.pack_r;
         s.Lk = a.cu_k[b + 1] - k_start;
-        qo = (int64_t)q_start * a.qs;
+        qo = (int64_t)q_start * a.qts;
         ko = a.bt ? 0 : (int64_t)k_start;  // paged: pages come from the table
         s.q = a.q + (qo + (int64_t)hq * a.qh) * ES;
         s.k = a.k + (ko * a.ks + (int64_t)hkv * a.kh) * ES;
         s.v = a.v + (ko * a.vs + (int64_t)hkv * a.vh) * ES;
-        s.o = a.o + ((int64_t)q_start * a.os + (int64_t)hq * a.oh) * OES;
+        s.o = a.o + ((int64_t)q_start * a.ots + (int64_t)hq * a.oh) * OES;
         s.lse = a.lse ? a.lse + (int64_t)hq * a.lse_h + q_start : nullptr;
     } else {
         s.Lq = a.Lq;

@@ -1485,11 +1485,16 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     // rows whose valid keys do not depend on their position -- no window, no
     // ALiBi; causal with one query row admits every key -- and, with the
     // per-row rescales of such rows, bit-identical to the unpacked call.
+    // Varlen calls whose longest query is one row pack the same way (a
+    // sequence's rows are its one token's query heads); there the lse rows
+    // of one token would not be contiguous, so only without an lse output.
+    const int64_t tok_qs = p->q_seq_stride, tok_os = p->o_seq_stride;  // token strides (varlen starts)
     mfa_fwd_params packed;
     bool pack = false;
-    if (p->dtype_in != MFA_DTYPE_F32 && !p->cu_seqlens_q && p->seqlen_q == 1 && p->heads_kv > 0 &&
-        p->heads_q > p->heads_kv && p->heads_q % p->heads_kv == 0 && p->window_left < 0 && p->window_right < 0 &&
-        !p->alibi_slopes && (!p->softmax_lse || p->lse_head_stride == 1) && p->tile_hint != MFA_TILE_PINGPONG) {
+    const bool lse_ok = p->cu_seqlens_q ? !p->softmax_lse : (!p->softmax_lse || p->lse_head_stride == 1);
+    if (p->dtype_in != MFA_DTYPE_F32 && p->seqlen_q == 1 && p->heads_kv > 0 && p->heads_q > p->heads_kv &&
+        p->heads_q % p->heads_kv == 0 && p->window_left < 0 && p->window_right < 0 && !p->alibi_slopes && lse_ok &&
+        p->tile_hint != MFA_TILE_PINGPONG) {
         const int R = p->heads_q / p->heads_kv;
         packed = *p;
         packed.seqlen_q = R;
@@ -1633,6 +1638,9 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     a.wr = p->window_right < 0 ? -1 : (int32_t)(p->window_right > wmax ? wmax : p->window_right);
     a.causal = p->causal ? 1 : 0;
     a.decode_pack = pack ? 1 : 0;
+    a.qts = tok_qs;
+    a.ots = tok_os;
+    a.pack_r = (pack && p->cu_seqlens_q) ? p->seqlen_q : 1;  // packed varlen: R rows per query token
     a.out_f32 = dout == MFA_DTYPE_F32 ? 1 : 0;
     a.lse = p->softmax_lse;
     a.lse_b = p->lse_batch_stride;

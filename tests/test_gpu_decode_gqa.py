@@ -45,3 +45,37 @@ def test_windows_and_alibi_keep_per_head_rows():
         ref = chunked.flash_attn_func(q.cpu(), k.cpu(), v.cpu(),
                                       **{x: (y.cpu() if torch.is_tensor(y) else y) for x, y in kw.items()})
         assert max_err(out, ref) <= REL_16_OUT * ref.abs().max().item(), kw
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("split", [0, None, 256])
+def test_packed_varlen_decode(dtype, split, monkeypatch):
+    # varlen decode (at most one query token per sequence; empty sequences too):
+    # bit-identical to repeated K/V heads and to each sequence's dense call
+    from gpu_util import make_varlen
+    from test_gpu_lse_paged import paginate
+
+    monkeypatch.setattr(_kernel, "_SPLIT_KEYS", split)
+    lens_q, lens_k = [1, 1, 0, 1, 1], [700, 4100, 9, 1, 2600]
+    q, k, v, cu_q, cu_k = make_varlen(lens_q, lens_k, 8, 2, 128, dtype, seed=20)
+    args = (cu_q, cu_k, 1, max(lens_k))
+    for kw in (dict(causal=True), dict(softcap=4.0)):
+        out = mfa.flash_attn_varlen_func(q, k, v, *args, **kw)
+        rep = mfa.flash_attn_varlen_func(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), *args, **kw)
+        assert torch.equal(out, rep), kw
+        pk, pv, table = paginate(k, v, lens_k, 512, seed=21)
+        paged = mfa.flash_attn_varlen_func(q, pk, pv, *args, block_table=table, **kw)
+        assert torch.equal(out, paged), kw
+        sq = [0] + torch.tensor(lens_q).cumsum(0).tolist()
+        sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()
+        for i in range(len(lens_q)):
+            if lens_q[i] == 0:
+                continue
+            dense = mfa.flash_attn_func(q[None, sq[i]:sq[i + 1]], k[None, sk[i]:sk[i + 1]], v[None, sk[i]:sk[i + 1]],
+                                        **kw)[0]
+            assert torch.equal(out[sq[i]:sq[i + 1]], dense), (kw, i)
+        ref = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), **kw)
+        assert max_err(out, ref) <= REL_16_OUT * ref.abs().max().item()
+    # with an lse output the varlen call keeps per-head rows (same values)
+    out2, lse = mfa.flash_attn_varlen_func_with_lse(q, k, v, *args, causal=True)
+    assert torch.equal(out2, mfa.flash_attn_varlen_func(q, k, v, *args, causal=True))
