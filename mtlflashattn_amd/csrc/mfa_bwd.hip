@@ -272,7 +272,11 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     typedef Ops<IS_BF16> O;
     typedef typename O::op_t op_t;
     constexpr int DS = DP / 16, DB = DP / 32;
-    constexpr int BQ = 32;       // query rows per step
+    // query rows per step: QSB 32-row sub-blocks (two where the registers
+    // allow two wavefronts per SIMD with them: the per-step barrier, staging
+    // and lse/Dsum loads then serve twice the MFMAs)
+    constexpr int QSB = DP <= 64 ? 2 : 1;
+    constexpr int BQ = 32 * QSB;
     constexpr int QST = DP + 8;  // LDS row stride of the Q / dO tiles (elements)
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
     constexpr int SCH = (BQ * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread and tensor
@@ -395,72 +399,85 @@ mfa_bwd_dkdv_kernel(BArgs a) {
             const uint16_t* qsb = q_s[buf];
             const uint16_t* dosb = do_s[buf];
 
-            // S = Q K^T and dP = dO V^T (lane = key, registers = query rows)
-            f32x16_t sacc, dpacc;
+            // S = Q K^T and dP = dO V^T per 32-row sub-block (lane = key,
+            // registers = query rows)
+            f32x16_t sacc[QSB], dpacc[QSB];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = dpacc[r] = 0.f;
+            for (int sb = 0; sb < QSB; ++sb)
 #pragma unroll
-            for (int s = 0; s < DS; ++s) {
-                const op_t qa = *reinterpret_cast<const op_t*>(qsb + l32 * QST + 16 * s + 8 * half);
-                const op_t da = *reinterpret_cast<const op_t*>(dosb + l32 * QST + 16 * s + 8 * half);
-                sacc = O::mfma(qa, kf[s], sacc);
-                dpacc = O::mfma(da, vf[s], dpacc);
-            }
-            // P and dS, rounded to 16 bits for the MFMAs; register r is query
-            // q0 + acc_row(r) + 4*half.  Tiles whose 32 x 32 pairs are all valid
-            // (wave-uniform test; lo/hi grow with the query) skip the masks.
+                for (int r = 0; r < 16; ++r) sacc[sb][r] = dpacc[sb][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < DS; ++s)
+#pragma unroll
+                for (int sb = 0; sb < QSB; ++sb) {
+                    const int row = 32 * sb + l32;
+                    const op_t qa = *reinterpret_cast<const op_t*>(qsb + row * QST + 16 * s + 8 * half);
+                    const op_t da = *reinterpret_cast<const op_t*>(dosb + row * QST + 16 * s + 8 * half);
+                    sacc[sb] = O::mfma(qa, kf[s], sacc[sb]);
+                    dpacc[sb] = O::mfma(da, vf[s], dpacc[sb]);
+                }
+            // Per sub-block: P and dS, rounded to 16 bits for the MFMAs (register
+            // r is query q0 + 32*sb + acc_row(r) + 4*half; tiles whose 32 x 32
+            // pairs are all valid, a wave-uniform test since lo/hi grow with
+            // the query, skip the masks), then the dV / dK products.
             const int wk0 = k0 + wave * 32;
-            const bool full = q0 + BQ <= Lq && key_lo(f, q0 + BQ - 1 + dq) <= wk0 && key_hi(f, q0 + dq, Lk) >= wk0 + 31;
-            uint32_t pw[8], dw[8];
-            auto probs = [&](auto masked_tag) {
-                constexpr bool MASKED = decltype(masked_tag)::value;
+            // (a compile-time loop: a run-time one, even unrolled, costs SGPR
+            // spills inside the step loop)
+            static_for<QSB>([&](auto sbc) __attribute__((always_inline)) {
+                constexpr int sb = decltype(sbc)::value;
+                uint32_t pw[8], dw[8];
+                const int qs0 = q0 + 32 * sb;
+                const bool full = qs0 + 32 <= Lq && key_lo(f, qs0 + 31 + dq) <= wk0 && key_hi(f, qs0 + dq, Lk) >= wk0 + 31;
+                auto probs = [&](auto masked_tag) {
+                    constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 l4 = *reinterpret_cast<const float4*>(lse_s[buf] + 8 * g + 4 * half);
-                    const float4 d4 = *reinterpret_cast<const float4*>(ds_s[buf] + 8 * g + 4 * half);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                    const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-                    float p[4], ds[4];
+                    for (int g = 0; g < 4; ++g) {
+                        const float4 l4 = *reinterpret_cast<const float4*>(lse_s[buf] + 32 * sb + 8 * g + 4 * half);
+                        const float4 d4 = *reinterpret_cast<const float4*>(ds_s[buf] + 32 * sb + 8 * g + 4 * half);
+                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+                        float p[4], ds[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int r = 4 * g + i;
-                        const int q = q0 + acc_row(r) + 4 * half;
-                        const int center = q + dq;
-                        float dcap;
-                        const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
-                        // (bitwise tests and an unconditional exp: selects, no branches)
-                        const float pe = fast_exp2(fmaf(x, c, -lv[i]));
-                        bool ok = true;
-                        if constexpr (MASKED)
-                            ok = (key <= key_hi(f, center, Lk)) & (key >= key_lo(f, center)) & (q < Lq);
-                        p[i] = ok ? pe : 0.f;
-                        ds[i] = p[i] * (dpacc[r] - dv4[i]);
-                        if constexpr (BIAS) ds[i] *= dcap;
+                        for (int i = 0; i < 4; ++i) {
+                            const int r = 4 * g + i;
+                            const int q = qs0 + acc_row(r) + 4 * half;
+                            const int center = q + dq;
+                            float dcap;
+                            const float x = transform<BIAS>(f, sacc[sb][r], slope, center - key, dcap);
+                            // (bitwise tests and an unconditional exp: selects, no branches)
+                            const float pe = fast_exp2(fmaf(x, c, -lv[i]));
+                            bool ok = true;
+                            if constexpr (MASKED)
+                                ok = (key <= key_hi(f, center, Lk)) & (key >= key_lo(f, center)) & (q < Lq);
+                            p[i] = ok ? pe : 0.f;
+                            ds[i] = p[i] * (dpacc[sb][r] - dv4[i]);
+                            if constexpr (BIAS) ds[i] *= dcap;
+                        }
+                        pw[2 * g] = O::pack(p[0], p[1]);
+                        pw[2 * g + 1] = O::pack(p[2], p[3]);
+                        dw[2 * g] = O::pack(ds[0], ds[1]);
+                        dw[2 * g + 1] = O::pack(ds[2], ds[3]);
                     }
-                    pw[2 * g] = O::pack(p[0], p[1]);
-                    pw[2 * g + 1] = O::pack(p[2], p[3]);
-                    dw[2 * g] = O::pack(ds[0], ds[1]);
-                    dw[2 * g + 1] = O::pack(ds[2], ds[3]);
-                }
-            };
-            if (full)
-                probs(std::false_type{});
-            else
-                probs(std::true_type{});
-            // dV^T += dO^T P, dK^T += Q^T dS: k-slots = query rows of accumulator
-            // registers 8*st..8*st+7 (rows 16*st + 4*half + 0..3, +8..11)
+                };
+                if (full)
+                    probs(std::false_type{});
+                else
+                    probs(std::true_type{});
+                // dV^T += dO^T P, dK^T += Q^T dS: k-slots = query rows of accumulator
+                // registers 8*st..8*st+7 (rows 32*sb + 16*st + 4*half + 0..3, +8..11)
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
-                const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
+                for (int st = 0; st < 2; ++st) {
+                    const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
+                    const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
 #pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    const op_t dot = O::load_tr(dosb, QST, 16 * st, 32 * db, lane);
-                    const op_t qt = O::load_tr(qsb, QST, 16 * st, 32 * db, lane);
-                    dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
-                    dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
+                    for (int db = 0; db < DB; ++db) {
+                        const op_t dot = O::load_tr(dosb, QST, 32 * sb + 16 * st, 32 * db, lane);
+                        const op_t qt = O::load_tr(qsb, QST, 32 * sb + 16 * st, 32 * db, lane);
+                        dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
+                        dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
+                    }
                 }
-            }
+            });
         }
         if (step + 1 < nsteps) swrite(buf ^ 1);  // the other stage was last read before the previous barrier
         __syncthreads();
