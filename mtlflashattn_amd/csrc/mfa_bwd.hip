@@ -276,6 +276,11 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     // allow two wavefronts per SIMD with them: the per-step barrier, staging
     // and lse/Dsum loads then serve twice the MFMAs)
     constexpr int QSB = DP <= 64 ? 2 : 1;
+    // At DP <= 64 (two wavefronts per SIMD, which hide the extra LDS read
+    // before the first MFMA) Dsum is staged negated and dP starts from it, so
+    // the accumulator ends as dP - Dsum; at larger DP Dsum is subtracted from
+    // the finished dP.
+    constexpr bool DFOLD = DP <= 64;
     constexpr int BQ = 32 * QSB;
     constexpr int QST = DP + 8;  // LDS row stride of the Q / dO tiles (elements)
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
@@ -367,7 +372,8 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         if (tid < BQ) {
             const bool in = q0 + tid < Lq;
             lreg = in ? lse2_of(qv.lse[q0 + tid]) : INFINITY;
-            dreg = in ? qv.dsum[q0 + tid] : 0.f;
+            const float dsv = in ? qv.dsum[q0 + tid] : 0.f;
+            dreg = DFOLD ? -dsv : dsv;
         }
     };
     auto swrite = [&](int buf) {
@@ -405,7 +411,16 @@ mfa_bwd_dkdv_kernel(BArgs a) {
 #pragma unroll
             for (int sb = 0; sb < QSB; ++sb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[sb][r] = dpacc[sb][r] = 0.f;
+                for (int g = 0; g < 4; ++g) {
+                    const float4 d4 = DFOLD ? *reinterpret_cast<const float4*>(ds_s[buf] + 32 * sb + 8 * g + 4 * half)
+                                            : float4{0.f, 0.f, 0.f, 0.f};
+                    dpacc[sb][4 * g] = d4.x;
+                    dpacc[sb][4 * g + 1] = d4.y;
+                    dpacc[sb][4 * g + 2] = d4.z;
+                    dpacc[sb][4 * g + 3] = d4.w;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sacc[sb][4 * g + i] = 0.f;
+                }
 #pragma unroll
             for (int s = 0; s < DS; ++s)
 #pragma unroll
@@ -433,8 +448,9 @@ mfa_bwd_dkdv_kernel(BArgs a) {
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const float4 l4 = *reinterpret_cast<const float4*>(lse_s[buf] + 32 * sb + 8 * g + 4 * half);
-                        const float4 d4 = *reinterpret_cast<const float4*>(ds_s[buf] + 32 * sb + 8 * g + 4 * half);
                         const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                        const float4 d4 = DFOLD ? float4{0.f, 0.f, 0.f, 0.f}
+                                                : *reinterpret_cast<const float4*>(ds_s[buf] + 32 * sb + 8 * g + 4 * half);
                         const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
                         float p[4], ds[4];
 #pragma unroll
@@ -450,7 +466,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
                             if constexpr (MASKED)
                                 ok = (key <= key_hi(f, center, Lk)) & (key >= key_lo(f, center)) & (q < Lq);
                             p[i] = ok ? pe : 0.f;
-                            ds[i] = p[i] * (dpacc[sb][r] - dv4[i]);
+                            ds[i] = DFOLD ? p[i] * dpacc[sb][r] : p[i] * (dpacc[sb][r] - dv4[i]);
                             if constexpr (BIAS) ds[i] *= dcap;
                         }
                         pw[2 * g] = O::pack(p[0], p[1]);
@@ -583,6 +599,10 @@ mfa_bwd_dq_kernel(BArgs a) {
     }
     const float lse2 = qin ? lse2_of(qv.lse[q]) : INFINITY;
     const float dsum = qin ? qv.dsum[q] : 0.f;
+    constexpr bool DFOLD = DP <= 64;  // registers allow the -Dsum vector
+    f32x16_t negd;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negd[r] = -dsum;
     const int center = q + dq;
     const int lo = key_lo(f, center), hi = key_hi(f, center, Lk);
     const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
@@ -649,9 +669,16 @@ mfa_bwd_dq_kernel(BArgs a) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             // S^T = K Q^T and dP^T = V dO^T (lane = query, registers = keys)
+            // (at DP <= 64 dP^T starts from -Dsum, a register vector the first
+            // MFMA reads as its C operand, so the accumulator ends as dP - Dsum)
             f32x16_t sacc, dpacc;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = dpacc[r] = 0.f;
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+            if constexpr (DFOLD)
+                dpacc = negd;
+            else
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dpacc[r] = 0.f;
 #pragma unroll
             for (int s = 0; s < DS; ++s) {
                 const op_t ka = *reinterpret_cast<const op_t*>(ksb + (32 * kb + l32) * KST + 16 * s + 8 * half);
@@ -676,7 +703,7 @@ mfa_bwd_dq_kernel(BArgs a) {
                         bool ok = true;
                         if constexpr (MASKED) ok = (key >= lo) & (key <= hi) & qin;
                         const float p = ok ? pe : 0.f;
-                        ds2[i] = p * (dpacc[r + i] - dsum);
+                        ds2[i] = DFOLD ? p * dpacc[r + i] : p * (dpacc[r + i] - dsum);
                         if constexpr (BIAS) ds2[i] *= dcap;
                     }
                     dw[kb][r / 2] = O::pack(ds2[0], ds2[1]);
