@@ -54,6 +54,9 @@ extern "C" {
 #define MFA_TILE_AUTO 0     /* library's choice */
 #define MFA_TILE_256 1      /* 256-row tiles, 4 wavefronts */
 #define MFA_TILE_PINGPONG 2 /* 512-row ping-pong tiles, 8 wavefronts (head_dim <= 64) */
+#define MFA_TILE_PINGPONG256 3 /* 256-row ping-pong tiles, 8 wavefronts (head_dim <= 64); the
+                                  library's choice for causal / windowed calls whose 512-row
+                                  tiles would leave CUs idle while the heaviest tiles finish */
 
 /*
  * Forward parameters.  Replaces the SH/PR/AL buffers of the reference

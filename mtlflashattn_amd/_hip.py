@@ -32,6 +32,7 @@ MFA_ERR_LAUNCH = -3
 MFA_TILE_AUTO = 0
 MFA_TILE_256 = 1
 MFA_TILE_PINGPONG = 2
+MFA_TILE_PINGPONG256 = 3
 
 DTYPE_CODES = {
     torch.float16: MFA_DTYPE_F16,

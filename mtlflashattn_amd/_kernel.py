@@ -48,6 +48,7 @@ _warned_modes = set()
 # cannot take (fp32; ping-pong with a head dim above 64 or a block table)
 # falls back to 0.
 _TILE_HINT = 0
+_PP_HINTS = (_hip.MFA_TILE_PINGPONG, _hip.MFA_TILE_PINGPONG256)
 # Split-KV chunk in keys for bf16/fp16 calls: None = the library's choice
 # (mfa_fwd_split_keys), 0 = never split, a multiple of 64 = that chunk
 # (tests and tuning).
@@ -250,7 +251,7 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and (Dp > 64 or paged is not None)):
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and (Dp > 64 or paged is not None)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     if lse is not None:
@@ -299,7 +300,7 @@ def _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, so
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and (Dp > 64 or paged is not None)):
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and (Dp > 64 or paged is not None)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     if lse_strides is not None:
@@ -312,7 +313,7 @@ def _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, so
 
 
 def _split_choice(p, dtype, hint):
-    if dtype == torch.float32 or hint == _hip.MFA_TILE_PINGPONG:
+    if dtype == torch.float32 or hint in _PP_HINTS:
         return 0
     return _hip.split_keys(p) if _SPLIT_KEYS is None else _SPLIT_KEYS
 
@@ -619,7 +620,7 @@ def launch_info(q, k, v, causal=False, softcap=0.0, alibi=False, window_left=-1,
     p.alibi_slopes = 256 if alibi else None
     p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint == _hip.MFA_TILE_PINGPONG and p.head_dim > 64):
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and p.head_dim > 64):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     return _hip.launch_info(p)

@@ -63,6 +63,7 @@ struct KArgs {
     int32_t U;        // (sequence, head) units = B * Hq
     int32_t upx;      // units per XCD (grouped schedule)
     int32_t grouped;  // 1: XCD-grouped by K/V head, 0: linear
+    int32_t tile_major;  // grouped order within an XCD: 1 tile-major, 0 unit-major
     // split-KV: the key range of a sequence is cut into chunks of split_keys
     // keys (a multiple of the key block); workgroup (tile, split) writes the
     // chunk's normalised O and log2-sum-exp to the workspace, the combine
@@ -176,11 +177,20 @@ __device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int
         // K/V head groups g = b*Hkv + hkv with g % 8 == x, all their q heads
         // and all their tiles.  Within an XCD the order is unit-major (all
         // tiles of one (sequence, q head), heaviest first, then the next), so
-        // the workgroups resident on the XCD share one head's K/V in its L2.
+        // the workgroups resident on the XCD share one head's K/V in its L2,
+        // when every tile costs the same; when tiles differ (causal, windows)
+        // it is tile-major (the heaviest tiles of every unit first), so the
+        // XCD's CUs take the work longest first and finish together.
         const int xcd = bid & 7;
         const int slot = bid >> 3;
-        const int j = slot / a.T;
-        tt = slot - j * a.T;
+        int j;
+        if (a.tile_major) {
+            tt = slot / a.upx;
+            j = slot - tt * a.upx;
+        } else {
+            j = slot / a.T;
+            tt = slot - j * a.T;
+        }
         const int R = a.Hq / a.Hkv;
         const int jg = j / R;
         const int g = xcd + 8 * jg;

@@ -38,6 +38,7 @@
 //    last query tiles) go first.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -1443,7 +1444,12 @@ KernelCfg cfg32(const char* name, bool paged) {
 #endif
 // paged K/V (block_table) runs on the 256-row and fp32 kernels only
 template <bool IS_BF16, bool BIAS>
-KernelCfg select16(int dp, bool fills_chip, bool paged) {
+KernelCfg select16(int dp, bool fills_chip, bool paged, bool pp256) {
+    if (MFA_PINGPONG && fills_chip && dp <= 64 && pp256) {  // one 32-row query block per wavefront
+        if (dp == 32)
+            return cfg16pp<32, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,1,2>" : "mfa_fwd16pp<f16,d32,1,2>");
+        return cfg16pp<64, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,1,2>" : "mfa_fwd16pp<f16,d64,1,2>");
+    }
     if (MFA_PINGPONG && fills_chip && dp <= 64) {
         if (dp == 32)
             return cfg16pp<32, 2, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,2,2>" : "mfa_fwd16pp<f16,d32,2,2>");
@@ -1477,6 +1483,43 @@ struct Plan {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Ping-pong tile height for dense causal / windowed calls, where tiles cost
+// different amounts.  Each choice's time is estimated as max(heaviest tile,
+// total work / CUs) -- what heaviest-first scheduling reaches -- in units of
+// one 512-row x 64-key block; a 256-row x 64-key block costs 0.545 of one
+// (the two tile heights' measured non-causal rates differ by 9%).  When the
+// 512-row tiles all run at once the heaviest sets the time, and 256-row
+// tiles, paired heavy with light on each CU, nearly halve it.
+constexpr int kChipCUs = 256;
+int64_t host_key_lo(const mfa_fwd_params* p, int64_t c) {
+    return p->window_left >= 0 ? std::max<int64_t>(c - p->window_left, 0) : 0;
+}
+int64_t host_key_hi(const mfa_fwd_params* p, int64_t c) {
+    int64_t hi = p->seqlen_k - 1;
+    if (p->causal) hi = std::min<int64_t>(hi, c);
+    if (p->window_right >= 0) hi = std::min<int64_t>(hi, c + p->window_right);
+    return hi;
+}
+double tile_makespan(const mfa_fwd_params* p, int rows, double block_cost) {
+    const int64_t dq = (int64_t)p->seqlen_k - p->seqlen_q;
+    const int64_t T = (p->seqlen_q + rows - 1) / rows;
+    int64_t heaviest = 0, total = 0;
+    for (int64_t t = 0; t < T; ++t) {
+        const int64_t r0 = t * rows, r1 = std::min<int64_t>(r0 + rows, p->seqlen_q) - 1;
+        const int64_t lo = host_key_lo(p, r0 + dq), hi = host_key_hi(p, r1 + dq);
+        const int64_t n = hi >= lo ? hi / 64 - lo / 64 + 1 : 0;
+        heaviest = std::max(heaviest, n);
+        total += n;
+    }
+    const double units = (double)p->batch * p->heads_q;
+    return std::max((double)heaviest, units * (double)total / kChipCUs) * block_cost;
+}
+bool prefer_pp256(const mfa_fwd_params* p) {
+    if (p->cu_seqlens_q || (!p->causal && p->window_left < 0 && p->window_right < 0)) return false;
+    if (p->seqlen_q > (1 << 20)) return false;  // (bounds the estimate's loop; long rows balance anyway)
+    return tile_makespan(p, 256, 0.545) < 0.9 * tile_makespan(p, 512, 1.0);
+}
+
 int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     if (!p) return set_err(MFA_ERR_INVALID, "mfa_fwd: params is NULL");
     // Single-row grouped-query decode: the R query heads of a K/V head become
@@ -1494,7 +1537,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     const bool lse_ok = p->cu_seqlens_q ? !p->softmax_lse : (!p->softmax_lse || p->lse_head_stride == 1);
     if (p->dtype_in != MFA_DTYPE_F32 && p->seqlen_q == 1 && p->heads_kv > 0 && p->heads_q > p->heads_kv &&
         p->heads_q % p->heads_kv == 0 && p->window_left < 0 && p->window_right < 0 && !p->alibi_slopes && lse_ok &&
-        p->tile_hint != MFA_TILE_PINGPONG) {
+        p->tile_hint != MFA_TILE_PINGPONG && p->tile_hint != MFA_TILE_PINGPONG256) {
         const int R = p->heads_q / p->heads_kv;
         packed = *p;
         packed.seqlen_q = R;
@@ -1576,9 +1619,10 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);
     // the 512-row ping-pong tiles are used when they still give every CU a
     // workgroup (256 CUs on MI355X)
-    if (p->tile_hint < MFA_TILE_AUTO || p->tile_hint > MFA_TILE_PINGPONG)
+    if (p->tile_hint < MFA_TILE_AUTO || p->tile_hint > MFA_TILE_PINGPONG256)
         return set_err(MFA_ERR_INVALID, "mfa_fwd: unknown tile_hint %d", p->tile_hint);
-    if (p->tile_hint == MFA_TILE_PINGPONG && (din == MFA_DTYPE_F32 || dp > 64))
+    const bool pp_hint = p->tile_hint == MFA_TILE_PINGPONG || p->tile_hint == MFA_TILE_PINGPONG256;
+    if (pp_hint && (din == MFA_DTYPE_F32 || dp > 64))
         return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles need bf16/fp16 and head_dim <= 64");
     // Auto: 512-row ping-pong tiles when they fill the chip (one workgroup
     // per CU) and leave at most 25% more rows empty than 256-row tiles do
@@ -1587,29 +1631,34 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     const int64_t rows256 = (int64_t)((p->seqlen_q + 255) / 256) * 256;
     bool fills_chip = p->tile_hint == MFA_TILE_AUTO
                           ? (int64_t)p->batch * p->heads_q * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256
-                          : p->tile_hint == MFA_TILE_PINGPONG;
+                          : pp_hint;
+    bool pp256 = p->tile_hint == MFA_TILE_PINGPONG256;
     if (split_keys != 0) {
         // split-KV runs on the 4-wavefront kernel (bf16/fp16)
         if (split_keys < 0 || split_keys % 64 != 0)
             return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: split_keys %d must be a positive multiple of 64",
                            split_keys);
         if (din == MFA_DTYPE_F32) return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd_splitkv: fp32 has no split-KV path");
-        if (p->tile_hint == MFA_TILE_PINGPONG)
+        if (pp_hint)
             return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd_splitkv: split-KV uses the 256-row tiles");
         fills_chip = false;
     }
     const bool paged = p->block_table != nullptr;
     if (paged) {
-        if (p->tile_hint == MFA_TILE_PINGPONG)
+        if (pp_hint)
             return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles do not take a block_table");
         fills_chip = false;
     }
+    if (p->tile_hint == MFA_TILE_AUTO && fills_chip && dp <= 64 && din != MFA_DTYPE_F32)
+        pp256 = prefer_pp256(p);
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp, paged) : select32<false>(dp, paged);
     else if (din == MFA_DTYPE_BF16)
-        plan->cfg = bias ? select16<true, true>(dp, fills_chip, paged) : select16<true, false>(dp, fills_chip, paged);
+        plan->cfg = bias ? select16<true, true>(dp, fills_chip, paged, pp256)
+                         : select16<true, false>(dp, fills_chip, paged, pp256);
     else
-        plan->cfg = bias ? select16<false, true>(dp, fills_chip, paged) : select16<false, false>(dp, fills_chip, paged);
+        plan->cfg = bias ? select16<false, true>(dp, fills_chip, paged, pp256)
+                         : select16<false, false>(dp, fills_chip, paged, pp256);
 
     KArgs& a = plan->args;
     memset(&a, 0, sizeof(a));
@@ -1673,6 +1722,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     const int64_t G = (int64_t)p->batch * p->heads_kv;
     if (G % 8 == 0 && G > 0) {
         a.grouped = 1;
+        a.tile_major = (p->causal || p->window_left >= 0 || p->window_right >= 0) ? 1 : 0;
         a.upx = (int32_t)(G / 8) * (p->heads_q / p->heads_kv);
         plan->grid = 8 * a.upx * a.T;
     } else {
@@ -1714,7 +1764,9 @@ constexpr int kSplitMaxLq = 256;
 constexpr int kSplitKeys = 2048;
 constexpr int64_t kSplitMaxUnits = 512;
 int auto_split_keys(const mfa_fwd_params* p) {
-    if (!p || p->dtype_in == MFA_DTYPE_F32 || p->tile_hint == MFA_TILE_PINGPONG) return 0;
+    if (!p || p->dtype_in == MFA_DTYPE_F32 || p->tile_hint == MFA_TILE_PINGPONG ||
+        p->tile_hint == MFA_TILE_PINGPONG256)
+        return 0;
     if (p->seqlen_q > kSplitMaxLq || p->seqlen_k <= kSplitKeys) return 0;
     if (!p->cu_seqlens_q && p->batch > 1 && (int64_t)p->batch * p->heads_q >= kSplitMaxUnits) return 0;
     return kSplitKeys;

@@ -86,7 +86,9 @@ def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
     (lambda p: setattr(p, "k_seq_stride", 68), _hip.MFA_ERR_INVALID, "strides"),
     (lambda p: setattr(p, "o", None), _hip.MFA_ERR_INVALID, "NULL"),
     (lambda p: setattr(p, "cu_seqlens_q", 256), _hip.MFA_ERR_INVALID, "cu_seqlens"),
-    (lambda p: setattr(p, "tile_hint", 3), _hip.MFA_ERR_INVALID, "tile_hint"),
+    (lambda p: setattr(p, "tile_hint", 4), _hip.MFA_ERR_INVALID, "tile_hint"),
+    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG256), setattr(p, "head_dim", 128),
+                setattr(p, "q_head_stride", 128)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
     (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "dtype_in", _hip.MFA_DTYPE_F32),
                 setattr(p, "dtype_out", _hip.MFA_DTYPE_F32)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
     (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "head_dim", 128),
@@ -154,6 +156,17 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     assert li.block_x == 512 and li.rows_per_block == 512
     p.tile_hint = _hip.MFA_TILE_256
     assert _hip.launch_info(p).block_x == 256
+    p.tile_hint = _hip.MFA_TILE_PINGPONG256
+    li = _hip.launch_info(p)
+    assert li.block_x == 512 and li.rows_per_block == 256
+    # causal: when every 512-row tile would run at once (256 of them here) the
+    # heaviest sets the time, and the 256-row ping-pong tiles are chosen
+    c8k = torch.empty(1, 8192, 16, 64, dtype=torch.bfloat16)
+    li = _kernel.launch_info(c8k, c8k, c8k, causal=True)
+    assert li.block_x == 512 and li.rows_per_block == 256, li.kernel_name
+    assert _kernel.launch_info(c8k, c8k, c8k).rows_per_block == 512  # non-causal: equal tiles
+    c16k = torch.empty(1, 16384, 16, 64, dtype=torch.bfloat16)  # 512 tiles: balanced by the schedule
+    assert _kernel.launch_info(c16k, c16k, c16k, causal=True).rows_per_block == 512
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
     info = _kernel.launch_info(f16, f16, f16, causal=True)
     assert info.kernel_name.startswith(b"mfa_fwd16<f16,d128")
@@ -221,6 +234,7 @@ def test_split_kv_workspace_size(lib):
     (1024, lambda p: setattr(p, "dtype_in", _hip.MFA_DTYPE_F32) or setattr(p, "dtype_out", _hip.MFA_DTYPE_F32),
      _hip.MFA_ERR_UNSUPPORTED, "fp32"),
     (1024, lambda p: setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), _hip.MFA_ERR_UNSUPPORTED, "256-row"),
+    (1024, lambda p: setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG256), _hip.MFA_ERR_UNSUPPORTED, "256-row"),
     (64, lambda p: setattr(p, "seqlen_k", 64 * 1025), _hip.MFA_ERR_INVALID, "exceed"),
     (192, lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 256), setattr(p, "num_pages", 16)),
      _hip.MFA_ERR_INVALID, "multiple of 256 with a block_table"),

@@ -20,10 +20,12 @@ pytestmark = pytest.mark.gpu
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
-@pytest.fixture(params=[_hip.MFA_TILE_256, _hip.MFA_TILE_PINGPONG], ids=["tile256", "pingpong"])
+@pytest.fixture(params=[_hip.MFA_TILE_256, _hip.MFA_TILE_PINGPONG, _hip.MFA_TILE_PINGPONG256],
+                ids=["tile256", "pingpong", "pingpong256"])
 def tile(request, monkeypatch):
-    """Run a test through each bf16/fp16 kernel: 256-row tiles and the 512-row
-    ping-pong tiles (head dims <= 64; other cases keep the library's choice)."""
+    """Run a test through each bf16/fp16 kernel: 256-row tiles and the 512- and
+    256-row ping-pong tiles (head dims <= 64; other cases keep the library's
+    choice)."""
     monkeypatch.setattr(_kernel, "_TILE_HINT", request.param)
     return request.param
 
@@ -273,6 +275,27 @@ class TestPacked:
         out_p = mfa.flash_attn_varlen_kvpacked_func(q, kv, cu_q, cu_k, 30, 60)
         k, v = kv.unbind(dim=1)
         assert torch.equal(out_p, mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 30, 60))
+
+
+@pytest.mark.parametrize("L,H,kw", [
+    (1000, 4, dict(causal=True)),
+    (1536, 2, dict(causal=True, window_size=(300, 0))),
+    (777, 3, dict(window_size=(100, 50), softcap=20.0)),
+    (2048, 2, dict(causal=True, alibi=True)),
+])
+def test_pingpong_tile_heights_bit_exact(monkeypatch, L, H, kw):
+    """The 512- and 256-row ping-pong tiles (the library picks the 256-row ones
+    for causal calls with few tiles) give the same bits: each 32-row query
+    block sees the same key blocks in the same order either way."""
+    q, k, v = make_qkv(2, L, L, H, H, 64, torch.bfloat16, seed=L)
+    kw = dict(kw)
+    if kw.pop("alibi", False):
+        kw["alibi_slopes"] = torch.rand(H, device="cuda") * 0.5
+    outs = []
+    for hint in (_hip.MFA_TILE_PINGPONG, _hip.MFA_TILE_PINGPONG256):
+        monkeypatch.setattr(_kernel, "_TILE_HINT", hint)
+        outs.append(mfa.flash_attn_func(q, k, v, **kw))
+    assert torch.equal(outs[0], outs[1])
 
 
 class TestBaselineConfigs:
