@@ -544,8 +544,11 @@ mfa_fwd16_kernel(KArgs a) {
         const int64_t kbo = kv_block_off<PAGED>(a, sv, j, kend, a.kb, a.ks, kok);
         const int64_t vbo = kv_block_off<PAGED>(a, sv, j, kend, a.vb, a.vs, vok);
         const int live = -(int)(rows > 0 && kok && vok);
-        const int kbytes = (int)(((int64_t)rm1 * a.ks + D) * 2) & live;
-        const int vbytes = (int)(((int64_t)rm1 * a.vs + D) * 2) & live;
+        // (readfirstlane: the sizes are uniform, but the clamp above selects
+        // a vector med3, and a resource the backend sees in vector registers
+        // gets a waterfall loop around every load)
+        const int kbytes = __builtin_amdgcn_readfirstlane((int)(((int64_t)rm1 * a.ks + D) * 2) & live);
+        const int vbytes = __builtin_amdgcn_readfirstlane((int)(((int64_t)rm1 * a.vs + D) * 2) & live);
         const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(sv.k + kbo * 2), (short)0, kbytes, kBufferDword3);
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
