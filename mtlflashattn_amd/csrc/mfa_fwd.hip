@@ -1460,7 +1460,13 @@ KernelCfg select16(int dp, bool fills_chip, bool paged, bool pp256) {
     }
     switch (dp) {
         case 32: return cfg16<32, MFA_D32_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d32," MFA_STR(MFA_D32_TILE) ">" : "mfa_fwd16<f16,d32," MFA_STR(MFA_D32_TILE) ">", paged);
-        case 64: return cfg16<64, MFA_D64_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64," MFA_STR(MFA_D64_TILE) ">" : "mfa_fwd16<f16,d64," MFA_STR(MFA_D64_TILE) ">", paged);
+        case 64:
+            // with a bias two query blocks per wavefront exceed the register
+            // budget and spill to scratch inside the loop (2.2-2.8x slower)
+            if constexpr (BIAS)
+                return cfg16<64, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64,1, 2>" : "mfa_fwd16<f16,d64,1, 2>", paged);
+            else
+                return cfg16<64, MFA_D64_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d64," MFA_STR(MFA_D64_TILE) ">" : "mfa_fwd16<f16,d64," MFA_STR(MFA_D64_TILE) ">", paged);
         case 96: return cfg16<96, MFA_D96_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d96," MFA_STR(MFA_D96_TILE) ">" : "mfa_fwd16<f16,d96," MFA_STR(MFA_D96_TILE) ">", paged);
         default: return cfg16<128, MFA_D128_TILE, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16<bf16,d128," MFA_STR(MFA_D128_TILE) ">" : "mfa_fwd16<f16,d128," MFA_STR(MFA_D128_TILE) ">", paged);
     }
