@@ -165,6 +165,10 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     li = _kernel.launch_info(c8k, c8k, c8k, causal=True)
     assert li.block_x == 512 and li.rows_per_block == 256, li.kernel_name
     assert _kernel.launch_info(c8k, c8k, c8k).rows_per_block == 512  # non-causal: equal tiles
+    # sliding windows, and causal calls with a bias, run on the 4-wavefront kernel
+    assert _kernel.launch_info(c8k, c8k, c8k, window_left=1024, window_right=0).block_x == 256
+    assert _kernel.launch_info(c8k, c8k, c8k, causal=True, softcap=30.0).block_x == 256
+    assert _kernel.launch_info(c8k, c8k, c8k, softcap=30.0).block_x == 512  # equal tiles: ping-pong
     c16k = torch.empty(1, 16384, 16, 64, dtype=torch.bfloat16)  # 512 tiles: balanced by the schedule
     assert _kernel.launch_info(c16k, c16k, c16k, causal=True).rows_per_block == 512
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
