@@ -49,6 +49,11 @@ _warned_modes = set()
 # falls back to 0.
 _TILE_HINT = 0
 _PP_HINTS = (_hip.MFA_TILE_PINGPONG, _hip.MFA_TILE_PINGPONG256)
+
+
+def _pp_head_dim_ok(D: int) -> bool:
+    """The ping-pong tiles exist for head dims padded to 32, 64 and 128 (not 96)."""
+    return -(-D // 32) * 32 != 96
 # Split-KV chunk in keys for bf16/fp16 calls: None = the library's choice
 # (mfa_fwd_split_keys), 0 = never split, a multiple of 64 = that chunk
 # (tests and tuning).
@@ -251,7 +256,7 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint in _PP_HINTS and (Dp > 64 or paged is not None)):
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and (not _pp_head_dim_ok(Dp) or paged is not None)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     if lse is not None:
@@ -300,7 +305,7 @@ def _prepare(q, k, v, out, batch, Hq, Hkv, Lq, Lk, Dp, varlen, scale, causal, so
     p.dtype_in = _hip.DTYPE_CODES[q.dtype]
     p.dtype_out = _hip.DTYPE_CODES[out.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint in _PP_HINTS and (Dp > 64 or paged is not None)):
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and (not _pp_head_dim_ok(Dp) or paged is not None)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     if lse_strides is not None:
@@ -620,7 +625,7 @@ def launch_info(q, k, v, causal=False, softcap=0.0, alibi=False, window_left=-1,
     p.alibi_slopes = 256 if alibi else None
     p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
     hint = _TILE_HINT
-    if q.dtype == torch.float32 or (hint in _PP_HINTS and p.head_dim > 64):
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and not _pp_head_dim_ok(p.head_dim)):
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     return _hip.launch_info(p)

@@ -1448,6 +1448,8 @@ KernelCfg cfg32(const char* name, bool paged) {
 // paged K/V (block_table) runs on the 256-row and fp32 kernels only
 template <bool IS_BF16, bool BIAS>
 KernelCfg select16(int dp, bool fills_chip, bool paged, bool pp256) {
+    if (MFA_PINGPONG && fills_chip && dp == 128)  // one 32-row query block per wavefront
+        return cfg16pp<128, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d128,1,2>" : "mfa_fwd16pp<f16,d128,1,2>");
     if (MFA_PINGPONG && fills_chip && dp <= 64 && pp256) {  // one 32-row query block per wavefront
         if (dp == 32)
             return cfg16pp<32, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,1,2>" : "mfa_fwd16pp<f16,d32,1,2>");
@@ -1631,16 +1633,27 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     if (p->tile_hint < MFA_TILE_AUTO || p->tile_hint > MFA_TILE_PINGPONG256)
         return set_err(MFA_ERR_INVALID, "mfa_fwd: unknown tile_hint %d", p->tile_hint);
     const bool pp_hint = p->tile_hint == MFA_TILE_PINGPONG || p->tile_hint == MFA_TILE_PINGPONG256;
-    if (pp_hint && (din == MFA_DTYPE_F32 || dp > 64))
-        return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles need bf16/fp16 and head_dim <= 64");
-    // Auto: 512-row ping-pong tiles when they fill the chip (one workgroup
-    // per CU) and leave at most 25% more rows empty than 256-row tiles do
-    // (short or single-row queries run faster on the 4-wavefront kernel).
+    if (pp_hint && (din == MFA_DTYPE_F32 || dp == 96))
+        return set_err(MFA_ERR_UNSUPPORTED,
+                       "mfa_fwd: ping-pong tiles need bf16/fp16 and head_dim <= 64 or 97..128");
+    // Auto: ping-pong tiles (512 rows at head dims <= 64, 256 at 128) when
+    // they fill the chip (one workgroup per CU) and leave at most 25% more
+    // rows empty than the 4-wavefront kernel's tiles (256 / 128 rows) do:
+    // short or single-row queries run faster on the 4-wavefront kernel.  At
+    // head dim 128 varlen and windowed calls stay on the 4-wavefront kernel
+    // too (measured: config 4 shapes 524 vs 559 us, config 5 861 vs 906).
     const int64_t rows512 = (int64_t)((p->seqlen_q + 511) / 512) * 512;
     const int64_t rows256 = (int64_t)((p->seqlen_q + 255) / 256) * 256;
-    bool fills_chip = p->tile_hint == MFA_TILE_AUTO
-                          ? (int64_t)p->batch * p->heads_q * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256
-                          : pp_hint;
+    const int64_t rows128 = (int64_t)((p->seqlen_q + 127) / 128) * 128;
+    const int64_t units = (int64_t)p->batch * p->heads_q;
+    bool fills_chip = pp_hint;
+    if (p->tile_hint == MFA_TILE_AUTO) {
+        if (dp == 128)
+            fills_chip = !p->cu_seqlens_q && p->window_left < 0 && p->window_right < 0 &&
+                         units * (rows256 / 256) >= 256 && 4 * rows256 <= 5 * rows128;
+        else
+            fills_chip = units * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256;
+    }
     bool pp256 = p->tile_hint == MFA_TILE_PINGPONG256;
     if (split_keys != 0) {
         // split-KV runs on the 4-wavefront kernel (bf16/fp16)

@@ -87,12 +87,12 @@ def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
     (lambda p: setattr(p, "o", None), _hip.MFA_ERR_INVALID, "NULL"),
     (lambda p: setattr(p, "cu_seqlens_q", 256), _hip.MFA_ERR_INVALID, "cu_seqlens"),
     (lambda p: setattr(p, "tile_hint", 4), _hip.MFA_ERR_INVALID, "tile_hint"),
-    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG256), setattr(p, "head_dim", 128),
-                setattr(p, "q_head_stride", 128)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
+    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG256), setattr(p, "head_dim", 96),
+                setattr(p, "q_head_stride", 96)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
     (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "dtype_in", _hip.MFA_DTYPE_F32),
                 setattr(p, "dtype_out", _hip.MFA_DTYPE_F32)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
-    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "head_dim", 128),
-                setattr(p, "q_head_stride", 128)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
+    (lambda p: (setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG), setattr(p, "head_dim", 80),
+                setattr(p, "q_head_stride", 80)), _hip.MFA_ERR_UNSUPPORTED, "ping-pong"),
     (lambda p: setattr(p, "k_seq_stride", -64), _hip.MFA_ERR_INVALID, "sequence strides"),
     (lambda p: (setattr(p, "block_table", 256), setattr(p, "page_block_size", 256), setattr(p, "num_pages", 4),
                 setattr(p, "tile_hint", _hip.MFA_TILE_PINGPONG)), _hip.MFA_ERR_UNSUPPORTED, "block_table"),
@@ -172,8 +172,13 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     c16k = torch.empty(1, 16384, 16, 64, dtype=torch.bfloat16)  # 512 tiles: balanced by the schedule
     assert _kernel.launch_info(c16k, c16k, c16k, causal=True).rows_per_block == 512
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
-    info = _kernel.launch_info(f16, f16, f16, causal=True)
-    assert info.kernel_name.startswith(b"mfa_fwd16<f16,d128")
+    info = _kernel.launch_info(f16, f16, f16, causal=True)  # dense, 512 tiles of 256 rows: ping-pong
+    assert info.kernel_name.startswith(b"mfa_fwd16pp<f16,d128") and info.rows_per_block == 256
+    # head dim 128: windowed calls and small grids stay on the 4-wavefront kernel
+    assert _kernel.launch_info(f16, f16, f16, window_left=256, window_right=256).kernel_name.startswith(
+        b"mfa_fwd16<f16,d128")
+    small128 = torch.empty(1, 2048, 16, 128, dtype=torch.float16)
+    assert _kernel.launch_info(small128, small128, small128).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     big = torch.empty(1, 32768, 16, 128, dtype=torch.bfloat16)
     info = _kernel.launch_info(big, big, big, causal=True, softcap=30.0, alibi=True, window_left=2048, window_right=0)
     assert info.kernel_name.endswith(b"+bias")
