@@ -940,12 +940,24 @@ mfa_fwd16_pp_kernel(KArgs a) {
         return;
     }
 
-    // ---- LDS tiles: chunk c of row r is stored in chunk slot c ^ swz(r)
-    // K: the 8 lanes of one ds_read_b128 cycle read one chunk of 8 rows;
-    // V: the 16 lanes of one ds_read_b64_tr_b16 cycle read 2 chunks of 4 rows
-    constexpr int kSw8 = CPR % 8 == 0;  // 128-byte multiple rows (else 64 B)
-    auto kswz = [](int r) { return kSw8 ? (r & 7) : ((r >> 1) & 3); };
-    auto vswz = [](int r) { return kSw8 ? 2 * (r & 3) : 2 * ((r >> 1) & 1); };
+    // ---- LDS tiles: chunk c of row r is stored in chunk slot c ^ swz(r).
+    // The LDS serves 256 bytes per cycle: the 16 lanes of one ds_read_b128
+    // cycle (one K row each, the same chunk index) and the 32 lanes of one
+    // ds_read_b64_tr_b16 cycle (4 V rows x 64 bytes) must fall in distinct
+    // 16-byte bank groups of a 256-byte line (SQ_LDS_BANK_CONFLICT = 0
+    // measured at head dims 64 and 128).  Rows are 256, 128 or 64 bytes:
+    // 1, 2 or 4 rows share a line, so the swizzle spreads rows that share
+    // a line position.
+    auto kswz = [](int r) {
+        if constexpr (CPR == 16) return r & 15;
+        else if constexpr (CPR == 8) return (r >> 1) & 7;
+        else return (r >> 2) & 3;
+    };
+    auto vswz = [](int r) {  // 4-chunk groups stay contiguous (multiples of 4)
+        if constexpr (CPR == 16) return 4 * (r & 3);
+        else if constexpr (CPR == 8) return 4 * ((r >> 1) & 1);
+        else return 0;
+    };
     uint16_t* const kst0 = smem;
     uint16_t* const vst0 = smem + NST * TILE;
     // direct-to-LDS loads: load i of wave w fills tile slots
