@@ -53,10 +53,12 @@ extern "C" {
 /* tile_hint values (bf16/fp16 only; fp32 has one kernel) */
 #define MFA_TILE_AUTO 0     /* library's choice */
 #define MFA_TILE_256 1      /* 256-row tiles, 4 wavefronts */
-#define MFA_TILE_PINGPONG 2 /* 512-row ping-pong tiles, 8 wavefronts (head_dim <= 64) */
-#define MFA_TILE_PINGPONG256 3 /* 256-row ping-pong tiles, 8 wavefronts (head_dim <= 64); the
-                                  library's choice for causal / windowed calls whose 512-row
-                                  tiles would leave CUs idle while the heaviest tiles finish */
+#define MFA_TILE_PINGPONG 2 /* ping-pong tiles, 8 wavefronts: 512 rows at head_dim <= 64,
+                               256 rows at head_dim 97..128 (not 65..96) */
+#define MFA_TILE_PINGPONG256 3 /* 256-row ping-pong tiles, 8 wavefronts (head_dim <= 64 or
+                                  97..128); the library's choice at head_dim <= 64 for causal
+                                  calls whose 512-row tiles would leave CUs idle while the
+                                  heaviest tiles finish */
 
 /*
  * Forward parameters.  Replaces the SH/PR/AL buffers of the reference
