@@ -1684,13 +1684,16 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
         fills_chip = false;
     }
     if (p->tile_hint == MFA_TILE_AUTO && fills_chip && dp <= 64 && din != MFA_DTYPE_F32) {
-        // Windowed calls, and causal calls with a soft-cap / ALiBi transform,
-        // run faster on the 4-wavefront kernel (measured at L=8192 H=16 D=64:
-        // window (2048,0) 99 vs 106 us, (256,256) 45 vs 55, causal + soft-cap
-        // 261 vs 305): a ping-pong workgroup's waves share one K/V stream,
-        // so rows whose window ends early wait through the rest of it.
+        // Windowed calls, causal calls with a soft-cap / ALiBi transform and
+        // varlen calls run faster on the 4-wavefront kernel (measured at
+        // L=8192 H=16 D=64: window (2048,0) 99 vs 106 us, (256,256) 45 vs
+        // 55, causal + soft-cap 261 vs 305; config 4's varlen lengths at
+        // D=64 Hq=32 Hkv=8: causal 306 vs 398 us, non-causal 512 vs 556): a
+        // ping-pong workgroup's waves share one K/V stream, so rows whose
+        // window ends early wait through the rest of it, and 512-row tiles
+        // leave much of a short sequence's last tile empty.
         const bool windowed = p->window_left >= 0 || p->window_right >= 0;
-        if (windowed || (p->causal && bias))
+        if (windowed || (p->causal && bias) || p->cu_seqlens_q)
             fills_chip = false;
         else
             pp256 = prefer_pp256(p);
