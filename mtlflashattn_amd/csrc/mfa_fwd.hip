@@ -1692,8 +1692,16 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
         // ping-pong workgroup's waves share one K/V stream, so rows whose
         // window ends early wait through the rest of it, and 512-row tiles
         // leave much of a short sequence's last tile empty.
+        // Causal calls whose 512-row tiles are few per head (<= 8) and take
+        // more than one round of workgroups go there as well (measured:
+        // B=8 L=1024 Hq=32 68 vs 97 us, B=2 L=4096 Hq=32 Hkv=8 172 vs 190;
+        // with one round, or longer rows, the ping-pong tiles win: L=4096
+        // H=32 100 vs 117, B=2 L=8192 H=16 327 vs 345).
         const bool windowed = p->window_left >= 0 || p->window_right >= 0;
+        const int64_t t512 = rows512 / 512;
         if (windowed || (p->causal && bias) || p->cu_seqlens_q)
+            fills_chip = false;
+        else if (p->causal && t512 <= 8 && units * t512 > 256)
             fills_chip = false;
         else
             pp256 = prefer_pp256(p);

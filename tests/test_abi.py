@@ -169,6 +169,10 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     assert _kernel.launch_info(c8k, c8k, c8k, window_left=1024, window_right=0).block_x == 256
     assert _kernel.launch_info(c8k, c8k, c8k, causal=True, softcap=30.0).block_x == 256
     assert _kernel.launch_info(c8k, c8k, c8k, softcap=30.0).block_x == 512  # equal tiles: ping-pong
+    # causal with few 512-row tiles per head over several rounds: 4-wavefront kernel
+    c1k = torch.empty(8, 1024, 32, 64, dtype=torch.bfloat16)
+    assert _kernel.launch_info(c1k, c1k, c1k, causal=True).block_x == 256
+    assert _kernel.launch_info(c1k, c1k, c1k).block_x == 512  # non-causal: ping-pong
     c16k = torch.empty(1, 16384, 16, 64, dtype=torch.bfloat16)  # 512 tiles: balanced by the schedule
     assert _kernel.launch_info(c16k, c16k, c16k, causal=True).rows_per_block == 512
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
