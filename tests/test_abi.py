@@ -181,6 +181,8 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     # head dim 128: windowed calls and small grids stay on the 4-wavefront kernel
     assert _kernel.launch_info(f16, f16, f16, window_left=256, window_right=256).kernel_name.startswith(
         b"mfa_fwd16<f16,d128")
+    short128 = torch.empty(16, 1024, 16, 128, dtype=torch.float16)  # 4 tiles per head
+    assert _kernel.launch_info(short128, short128, short128, causal=True).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     small128 = torch.empty(1, 2048, 16, 128, dtype=torch.float16)
     assert _kernel.launch_info(small128, small128, small128).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     big = torch.empty(1, 32768, 16, 128, dtype=torch.bfloat16)
