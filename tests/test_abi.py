@@ -170,6 +170,10 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     assert _kernel.launch_info(c8k, c8k, c8k, causal=True, softcap=30.0).block_x == 256
     assert _kernel.launch_info(c8k, c8k, c8k, softcap=30.0).block_x == 512  # equal tiles: ping-pong
     # causal with few 512-row tiles per head over several rounds: 4-wavefront kernel
+    c4k = torch.empty(1, 4096, 16, 64, dtype=torch.bfloat16)  # 128 tiles of 512 rows, 256 of 256
+    li = _kernel.launch_info(c4k, c4k, c4k, causal=True)
+    assert li.block_x == 512 and li.rows_per_block == 256
+    assert _kernel.launch_info(c4k, c4k, c4k).block_x == 256  # non-causal: 4-wavefront kernel
     c1k = torch.empty(8, 1024, 32, 64, dtype=torch.bfloat16)
     assert _kernel.launch_info(c1k, c1k, c1k, causal=True).block_x == 256
     assert _kernel.launch_info(c1k, c1k, c1k).block_x == 512  # non-causal: ping-pong
