@@ -1685,13 +1685,16 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
             return set_err(MFA_ERR_UNSUPPORTED, "mfa_fwd: ping-pong tiles do not take a block_table");
         fills_chip = false;
     }
-    // Dense causal calls (no window, no bias) whose 512-row tiles do not fill
-    // the chip but whose 256-row ping-pong tiles do: those tiles (measured
-    // 15-25% faster than the 4-wavefront kernel: B=1 L=4096 H=16 D=64 101 ->
-    // 80 us, B=1 L=8192 H=8 187 -> 146, B=4 L=1024 H=16 36 -> 30).
+    // Dense calls (no window, no bias) of rows >= 1024 whose 512-row tiles do
+    // not fill the chip but whose 256-row ping-pong tiles do: those tiles (measured 15-25%
+    // faster than the 4-wavefront kernel at D=64: causal B=1 L=4096 H=16 101
+    // -> 80 us, B=1 L=8192 H=8 187 -> 146; non-causal B=1 L=4096 H=16 100 ->
+    // 83, B=1 L=8192 H=8 188 -> 156).
     if (p->tile_hint == MFA_TILE_AUTO && !fills_chip && !paged && split_keys == 0 && dp <= 64 &&
-        din != MFA_DTYPE_F32 && p->causal && !bias && !p->cu_seqlens_q && p->window_left < 0 &&
-        p->window_right < 0 && units * (rows256 / 256) >= 256) {
+        din != MFA_DTYPE_F32 && !bias && !p->cu_seqlens_q && p->window_left < 0 && p->window_right < 0 &&
+        units * (rows256 / 256) >= 256 && rows256 / 256 >= 4) {
+        // (rows of >= 4 tiles: shorter rows, e.g. B=64 L=256 H=16, run 40 vs
+        // 50 us on the 4-wavefront kernel)
         fills_chip = true;
         pp256 = true;
     } else if (p->tile_hint == MFA_TILE_AUTO && fills_chip && dp <= 64 && din != MFA_DTYPE_F32) {

@@ -147,6 +147,7 @@ def test_launch_geometry_of_the_baseline_configs(lib):
         qs = torch.empty(64, lq, 16, 64, dtype=torch.bfloat16)
         ks = torch.empty(64, lk, 16, 64, dtype=torch.bfloat16)
         assert _kernel.launch_info(qs, ks, ks).block_x == 256, (lq, lk)
+        assert _kernel.launch_info(qs, ks, ks, causal=True).block_x == 256, (lq, lk)
     long = torch.empty(8, 1280, 16, 64, dtype=torch.bfloat16)
     assert _kernel.launch_info(long, long, long).block_x == 512
     # the tile hint overrides the automatic choice
@@ -173,7 +174,8 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     c4k = torch.empty(1, 4096, 16, 64, dtype=torch.bfloat16)  # 128 tiles of 512 rows, 256 of 256
     li = _kernel.launch_info(c4k, c4k, c4k, causal=True)
     assert li.block_x == 512 and li.rows_per_block == 256
-    assert _kernel.launch_info(c4k, c4k, c4k).block_x == 256  # non-causal: 4-wavefront kernel
+    assert _kernel.launch_info(c4k, c4k, c4k).rows_per_block == 256  # non-causal: the same tiles
+    assert _kernel.launch_info(c4k, c4k, c4k, softcap=30.0).block_x == 256  # bias: 4-wavefront kernel
     c1k = torch.empty(8, 1024, 32, 64, dtype=torch.bfloat16)
     assert _kernel.launch_info(c1k, c1k, c1k, causal=True).block_x == 256
     assert _kernel.launch_info(c1k, c1k, c1k).block_x == 512  # non-causal: ping-pong
