@@ -14,6 +14,9 @@ Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
   cpu_baseline : the reference's chunked-fp32 torch path (oracle/chunked.py)
                  timed on this host's cores on a bounded sample of the same
                  workload (a subset of heads).
+Before the W warm-up steps the step also runs untimed for --clock-warmup
+seconds (default 1.0, declared in the line as clock_warmup_s/_steps) so that
+the K timed steps see the steady-state shader clock.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7|8]
 (6-8: HBM-bound short-L shapes, roofline in GB/s against 8 TB/s; 8 runs split-KV)
 """
@@ -142,6 +145,20 @@ def run_step(c):
     return mfa.flash_attn_func(c["q"], c["k"], c["v"], **c["kw"])
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (the `Model name` lscpu prints, from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(cfg: int, budget_s: float = 12.0):
     """Oracle (reference chunked-fp32 torch path) on host cores, bounded sample."""
     import torch
@@ -192,7 +209,7 @@ def cpu_baseline(cfg: int, budget_s: float = 12.0):
         times.append(time.perf_counter() - t0)
     med = sorted(times)[1]
     return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": sample, "seconds": round(med, 3),
+            "model": cpu_model(), "sample": sample, "seconds": round(med, 3),
             "note": "formula FLOPs of the sample (4*H*Lq*Lk*D, halved for causal) / median of 3 runs"}
 
 
@@ -235,6 +252,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8, 9],
                     help="BASELINE config 2-5 (default 2, the headline); 6-9 are HBM-bound short-L / decode "
                          "shapes (roofline in GB/s; 8 runs split-KV, 9 is grouped-query decode)")
+    ap.add_argument("--clock-warmup", type=float, default=1.0,
+                    help="seconds of untimed back-to-back steps before the W warm-up steps, so the timed steps "
+                         "run at the steady-state shader clock (reported as clock_warmup_s / _steps)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--backward", action="store_true",
                     help="time the HIP backward (dq, dk, dv) of the config instead of the forward (configs 2-5; "
@@ -261,6 +281,20 @@ def main():
         step = make_backward_step(c)
         c = dict(c, formula=c["formula"] * 5 // 2, algo=c["algo"] * 5 // 2)
         args.no_cpu_baseline = True
+    # Clock warm-up, untimed and declared in the output line: the shader
+    # clock ramps up over the first ~0.1-0.5 s of load, so a few warm-up
+    # steps alone would leave the timed steps running during the ramp.  The
+    # same step runs back to back until `--clock-warmup` seconds of wall
+    # time have passed; then the W warm-up steps and the K timed steps follow
+    # unchanged.
+    clock_steps = 0
+    t_cw = time.perf_counter()
+    while time.perf_counter() - t_cw < args.clock_warmup:
+        for _ in range(8):
+            step()
+        clock_steps += 8
+        torch.cuda.synchronize()
+    clock_s = time.perf_counter() - t_cw
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -310,6 +344,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup_s": round(clock_s, 3),
+        "clock_warmup_steps": clock_steps,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -1,9 +1,15 @@
 """MI355X-native flash-attention forward for PyTorch-ROCm -- CUDA flash-attn API surface.
 
 Drop-in for mtlflashattn's public API (metal_flash_attn/__init__.py): the same
-six functions, argument meanings and error contract.  Inference-only (no
-backward).  Unsupported features raise NotImplementedError so callers can fall
-back, rather than silently approximating (metal_flash_attn/__init__.py:1-5).
+six functions, argument meanings and error contract.  Unsupported features
+raise NotImplementedError so callers can fall back, rather than silently
+approximating (metal_flash_attn/__init__.py:1-5).
+
+Backward: the reference is inference-only (metal_flash_attn/__init__.py:3-4).
+Here bf16/fp16 calls whose inputs require grad are differentiable through
+HIP backward kernels (dq, dk, dv; the returned lse too).  fp32 inputs and
+paged K/V stay forward-only: their backward raises NotImplementedError, as
+do dropout_p > 0, deterministic=True and return_attn_probs=True.
 
 Two additions the reference raises for: `flash_attn_varlen_func` accepts a
 paged K/V cache (`block_table`, CUDA flash-attn's layout), and
@@ -17,6 +23,7 @@ ROCm device; there is no CPU path.
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 
@@ -113,11 +120,7 @@ def flash_attn_func_with_lse(q, k, v, softmax_scale=None, causal=False, window_s
 def _dense(q, k, v, softmax_scale, causal, window_size, softcap, alibi_slopes, return_lse):
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError(f"mtlflashattn_amd: expected 4-D [B,S,H,D] tensors, got q.dim()={q.dim()}")
-    Hq, Hkv = q.shape[2], k.shape[2]
-    if Hkv == 0 or Hq % Hkv != 0:
-        raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
-    if k.shape[1] != v.shape[1]:
-        raise ValueError("mtlflashattn_amd: k/v seqlen mismatch")
+    _kernel._check_qkv_shapes(q, k, v, h_axis=2, s_axis=1)
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     return forward_bshd(
         q, k, v, scale=scale, causal=causal, softcap=softcap,
@@ -228,12 +231,18 @@ def _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_s
 
 
 def _check_block_table(block_table, lens_k, page, num_pages):
-    """Every page a sequence uses must exist (one host read of the table)."""
+    """The table has a column for every page a sequence uses (from the key
+    counts already on the host).  The page ids themselves are read on the
+    host only with MTLFLASHATTN_CHECK_PAGES=1 (a device-to-host copy and a
+    stream sync per call); otherwise the kernel's guard applies: a page id
+    outside [0, num_pages) reads as zeros, never out of bounds."""
     need = [-(-n // page) for n in lens_k]
     if max(need, default=0) > block_table.shape[1]:
         raise ValueError(f"mtlflashattn_amd: block_table has {block_table.shape[1]} pages per sequence, "
                          f"{max(need)} needed for {max(lens_k)} keys")
     if not need or max(need) == 0:
+        return
+    if os.environ.get("MTLFLASHATTN_CHECK_PAGES", "").lower() not in ("1", "on", "true", "yes"):
         return
     used = torch.arange(block_table.shape[1]).unsqueeze(0) < torch.tensor(need).unsqueeze(1)
     ids = block_table.cpu()[used]

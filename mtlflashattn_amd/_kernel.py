@@ -140,6 +140,24 @@ def _alibi_arg(alibi_slopes, B, Hq, device):
     return s.to(device=device, dtype=torch.float32).contiguous(), bstride
 
 
+def _check_qkv_shapes(q, k, v, h_axis, s_axis):
+    """4-D q/k/v that agree on the batch size, k/v on head count and length,
+    and a K/V head count that divides the query head count (CUDA flash-attn
+    and stock SDPA reject the rest; the kernel takes B from q and the K/V
+    head count from k, so a mismatch must never reach it)."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError(f"mtlflashattn_amd: expected 4-D q/k/v, got {q.dim()}/{k.dim()}/{v.dim()} dims")
+    if not (q.shape[0] == k.shape[0] == v.shape[0]):
+        raise ValueError(f"mtlflashattn_amd: batch mismatch (q {q.shape[0]}, k {k.shape[0]}, v {v.shape[0]})")
+    Hq, Hkv = q.shape[h_axis], k.shape[h_axis]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
+    if v.shape[h_axis] != Hkv:
+        raise ValueError(f"mtlflashattn_amd: k has {Hkv} heads, v {v.shape[h_axis]}")
+    if k.shape[s_axis] != v.shape[s_axis]:
+        raise ValueError("mtlflashattn_amd: k/v seqlen mismatch")
+
+
 def _is_rocm_tensor(t) -> bool:
     """True for a tensor on a ROCm GPU (the only device the HIP path serves)."""
     return t.device.type == "cuda" and torch.version.hip is not None
@@ -363,10 +381,8 @@ def flash_attn_forward(q, k, v, scale, causal, softcap=0.0, window_left=-1, wind
     if softcap < 0:
         # _kernel.py:1070-1073: reject here so direct callers cannot diverge
         raise ValueError("mtlflashattn_amd: softcap must be >= 0 (0 disables capping)")
+    _check_qkv_shapes(q, k, v, h_axis=1, s_axis=2)
     B, Hq, Lq, D = q.shape
-    Hkv = k.shape[1]
-    if Hkv == 0 or Hq % Hkv != 0:
-        raise ValueError(f"mtlflashattn_amd: num_heads_kv ({Hkv}) must divide num_heads_q ({Hq})")
     alibi, bstride = _alibi_arg(alibi_slopes, B, Hq, q.device)
     _check_device(q, k, v)
     if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -400,6 +416,7 @@ def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_rig
         _record_trace(q.dtype, q.shape[-1], q.shape[1], k.shape[1], causal)
     if softcap < 0:
         raise ValueError("mtlflashattn_amd: softcap must be >= 0 (0 disables capping)")
+    _check_qkv_shapes(q, k, v, h_axis=2, s_axis=1)
     B, Lq, Hq, D = q.shape
     if _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
         _alibi_arg(alibi_slopes, B, Hq, q.device)  # validate before autograd records anything
@@ -437,6 +454,9 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
     alibi, bstride = _alibi_arg(alibi_slopes, batch, Hq, q.device)
     if _trace_enabled() and _grad:
         _record_trace(q.dtype, q.shape[-1], max_q, max_k, causal, "hip-varlen")
+    if block_table is not None and _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
+        raise NotImplementedError("mtlflashattn_amd: paged K/V (block_table) calls are forward-only; "
+                                  "run them under torch.no_grad() or without inputs that require grad")
     if _grad and block_table is None and _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
         o, lse = _FlashAttnVarlenFn.apply(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left,
                                           window_right, alibi_slopes)

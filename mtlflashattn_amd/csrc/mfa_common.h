@@ -112,14 +112,19 @@ __device__ __forceinline__ float sum_halves(float x) {
 // before later LDS reads it cannot prove disjoint.  The caller waits (vmcnt) before a
 // barrier that publishes the data.  The resource is a raw buffer: base
 // address, stride 0, `bytes` records, dword3 0x00020000.
+// M0 carries the LDS address.  It is an input operand bound to M0 itself
+// ("{m0}"): the compiler writes M0 before the statement and knows what it
+// holds afterwards (the asm only reads it), so M0 is neither written by the
+// asm nor in its clobber list.  (s_nop 0: one wait state between the M0
+// write and the load that reads it.)
 __device__ __forceinline__ void lds_load16(uint64_t base, uint32_t bytes, uint16_t* dst, uint32_t off) {
     typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t rsrc_t;
     const rsrc_t r = {(uint32_t)base, (uint32_t)(base >> 32) & 0xffffu, bytes, (uint32_t)kBufferDword3};
-    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
-                 : "s"(m0), "v"(off), "s"(r)
-                 : "memory", "m0");
+                 : "v"(off), "s"(r), "{m0}"(lds)
+                 : "memory");
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>{}) for I = 0 .. N-1.

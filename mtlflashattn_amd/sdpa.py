@@ -21,8 +21,7 @@ The fast-tier floor and tiers are re-derived for ROCm (the reference's 1024
 floor and its tier set were measured against stock MPS SDPA): on MI355X with
 torch 2.10 the HIP path matches or beats stock SDPA from 512 tokens in
 fp16/bf16 (0.94-2.3x at 512, 1.0-2.0x beyond) and from 256 in fp32, and loses
-below 512 in fp16/bf16 (host launch cost dominates there).  Re-measure on
-another machine with `python -m mtlflashattn_amd.sdpa_sweep`.
+below 512 in fp16/bf16 (host launch cost dominates there).
 
 Value head dim != query/key head dim (the reference's uneven-V shield,
 metal_flash_attn/sdpa.py:76-130, :145-149, an exact torch path): gated like
@@ -102,8 +101,14 @@ def _eligibility(q, k, v, attn_mask, dropout_p, is_causal):
     Hq, Hkv = q.shape[1], k.shape[1]
     if Hkv == 0 or Hq % Hkv != 0:
         return False, f"heads({Hq}/{Hkv})"
+    if not (q.shape[0] == k.shape[0] == v.shape[0]) or v.shape[1] != Hkv:
+        return False, "batch-or-heads-mismatch"
     if k.shape[2] != v.shape[2]:
         return False, "kv-len-mismatch"
+    # the HIP backward takes bf16/fp16 only: fp32 calls that autograd will
+    # differentiate stay on stock SDPA (its gradients flow)
+    if q.dtype == torch.float32 and torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return False, "grad-fp32"
     Lq, Lk = q.shape[2], k.shape[2]
     # SDPA's is_causal is TOP-LEFT aligned, the kernel's BOTTOM-RIGHT: equal only when Lq == Lk
     if is_causal and Lq != Lk:

@@ -96,6 +96,26 @@ class TestAfterDeviceCheck:
             mfa.flash_attn_func(t(1, 8, 4, 64), t(1, 9, 4, 64), t(1, 8, 4, 64))
         assert not fake_device
 
+    def test_batch_and_value_head_mismatch(self, fake_device):
+        # the kernel takes the batch from q and the K/V head count from k: a
+        # k/v batch or a v head count that differs must raise, never launch
+        with pytest.raises(ValueError, match="batch"):
+            mfa.flash_attn_func(t(4, 8, 4, 64), t(2, 8, 4, 64), t(2, 8, 4, 64))
+        with pytest.raises(ValueError, match="batch"):
+            mfa.flash_attn_func(t(2, 8, 4, 64), t(2, 8, 4, 64), t(1, 8, 4, 64))
+        with pytest.raises(ValueError, match="heads"):
+            mfa.flash_attn_func(t(1, 8, 4, 64), t(1, 8, 2, 64), t(1, 8, 1, 64))
+        # heads-second boundary and the heads-third launcher check the same
+        with pytest.raises(ValueError, match="batch"):
+            _kernel.flash_attn_forward(t(4, 4, 8, 32), t(2, 4, 8, 32), t(2, 4, 8, 32), 0.25, False)
+        with pytest.raises(ValueError, match="heads"):
+            _kernel.flash_attn_forward(t(1, 4, 8, 32), t(1, 2, 8, 32), t(1, 1, 8, 32), 0.25, False)
+        with pytest.raises(ValueError, match="seqlen"):
+            _kernel.flash_attn_forward(t(1, 4, 8, 32), t(1, 4, 8, 32), t(1, 4, 9, 32), 0.25, False)
+        with pytest.raises(ValueError, match="batch"):
+            _kernel.forward_bshd(t(3, 8, 4, 32), t(1, 8, 4, 32), t(1, 8, 4, 32), 0.25, False)
+        assert not fake_device
+
     def test_default_scale_and_forwarded_arguments(self, fake_device):
         q, k, v = t(2, 10, 8, 48), t(2, 12, 2, 48), t(2, 12, 2, 48)
         slopes = torch.rand(8)
@@ -149,7 +169,7 @@ class TestVarlenContract:
         with pytest.raises(NotImplementedError):
             mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6, dropout_p=0.5)
 
-    def test_block_table_contract(self, fake_device):
+    def test_block_table_contract(self, fake_device, monkeypatch):
         # the reference raises NotImplementedError for block_table
         # (metal_flash_attn/__init__.py:130-131); this build implements the paged
         # layout of CUDA flash-attn and validates it before any launch
@@ -164,9 +184,10 @@ class TestVarlenContract:
             mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6, block_table=bt.long())
         with pytest.raises(ValueError):  # one row per sequence
             mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6, block_table=bt[:1])
-        with pytest.raises(ValueError):  # page id outside the pool
-            mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6,
-                                       block_table=torch.tensor([[0], [3]], dtype=torch.int32))
+        bad_ids = torch.tensor([[0], [3]], dtype=torch.int32)
+        monkeypatch.setenv("MTLFLASHATTN_CHECK_PAGES", "1")
+        with pytest.raises(ValueError):  # page id outside the pool (host check on request)
+            mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6, block_table=bad_ids)
         with pytest.raises(ValueError):  # too few pages for 300 keys
             mfa.flash_attn_varlen_func(q, pool, pool, cu_q, torch.tensor([0, 300, 303], dtype=torch.int32),
                                        7, 300, block_table=bt)
@@ -177,6 +198,13 @@ class TestVarlenContract:
         call = fake_device[-1]
         assert out.shape == q.shape and call["k"].shape == pool.shape and call["block_table"] is not None
         assert call["seqlen_k"] == 6 and call["lse"] is None
+        # by default the page ids are not read on the host (no per-call device
+        # sync): an id outside the pool reaches the kernel, whose guard reads
+        # zeros for it
+        monkeypatch.delenv("MTLFLASHATTN_CHECK_PAGES")
+        n = len(fake_device)
+        mfa.flash_attn_varlen_func(q, pool, pool, cu_q, cu_k, 7, 6, block_table=bad_ids)
+        assert len(fake_device) == n + 1
 
     def test_with_lse_layouts(self, fake_device):
         q, k, v, cu_q, cu_k = self.make()

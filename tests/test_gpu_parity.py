@@ -299,7 +299,7 @@ def test_pingpong_tile_heights_bit_exact(monkeypatch, L, H, kw):
 
 
 class TestBaselineConfigs:
-    """BASELINE configs 2-4 at full size against the oracle (seconds of CPU each)."""
+    """BASELINE configs 2-5 at full size against the oracle (seconds of CPU each)."""
 
     def test_config2_bf16_d64_l8192(self):
         q, k, v = make_qkv(1, 8192, 8192, 16, 16, 64, torch.bfloat16, seed=1)
@@ -327,3 +327,35 @@ class TestBaselineConfigs:
         e32 = assert_parity(out32, ref, torch.bfloat16, "config4")
         eout = assert_output(out, ref, torch.bfloat16, "config4")
         print(f"config4 bf16 varlen: fp32-out {e32:.3e}, bf16-out {eout:.3e}, max|ref| {ref.abs().max():.3f}")
+
+    def test_config5_long_feature_mix_full_workload(self):
+        """Config 5 at its workload: bf16 B=1 L=32768 H=16 D=128, causal, window
+        (2048, 0), soft-cap 30, ALiBi 2^(-8(i+1)/16), inputs N(0,1)*0.5 from
+        seed 4 (the reference's op order, _kernel.py:1188-1207: soft-cap
+        :1191-1192 -> ALiBi :1193-1196 -> window masks :1201-1204).  The kernel
+        runs on the whole sequence; the oracle checks five 512-row chunks of
+        every head (before the window fills, as it fills, just after, the
+        middle, the tail) one head at a time, which bounds its host memory."""
+        L, H, D = 32768, 16, 128
+        q, k, v = make_qkv(1, L, L, H, H, D, torch.bfloat16, seed=4, scale_inputs=0.5)
+        slopes = torch.tensor([2 ** (-8 * (i + 1) / 16) for i in range(H)], dtype=torch.float32, device="cuda")
+        kw = dict(causal=True, window_size=(2048, 0), softcap=30.0, alibi_slopes=slopes)
+        out, out32 = run_both(q, k, v, **kw)
+        torch.cuda.synchronize()
+        chunk = 512
+        starts = (0, 1536, 2048, 16384, L - chunk)
+        rows = torch.cat([torch.arange(s0, s0 + chunk) for s0 in starts])
+        qc, kc, vc, sc = q.cpu(), k.cpu(), v.cpu(), slopes.cpu()
+        refs = []
+        for h in range(H):
+            ref = chunked.flash_attn_func(qc[:, :, h:h + 1], kc[:, :, h:h + 1], vc[:, :, h:h + 1], causal=True,
+                                          window_size=(2048, 0), softcap=30.0, alibi_slopes=sc[h:h + 1],
+                                          chunk=chunk, rows=set(starts))
+            refs.append(ref[0, rows, 0])
+        ref = torch.stack(refs, dim=1)  # [rows, H, D]
+        assert not torch.isnan(ref).any()
+        e32 = assert_parity(out32[0, rows], ref, torch.bfloat16, "config5 (fp32 output)")
+        eout = assert_output(out[0, rows], ref, torch.bfloat16, "config5 (bf16 output)")
+        rmax = ref.abs().max().item()
+        print(f"config5 bf16: fp32-out err {e32:.3e} ({e32 / rmax:.3e} max|ref|), bf16-out {eout:.3e} "
+              f"({eout / rmax:.3e} max|ref|), max|ref| {rmax:.3f}, rows checked {rows.numel()} x {H} heads")

@@ -66,8 +66,29 @@ class TestGates:
             assert self.elig(big, big, big)[1].startswith("head_dim")
             assert self.elig(q, q[:, :3], q[:, :3])[1].startswith("heads")
             assert self.elig(q, q, q[:, :, :32]) == (False, "kv-len-mismatch")
+            # batch / value-head mismatches stay on stock SDPA (the kernel
+            # would read past the K/V allocation)
+            q4 = torch.zeros(4, 4, 64, 64, dtype=torch.float16)
+            k2 = torch.zeros(2, 4, 64, 64, dtype=torch.float16)
+            assert self.elig(q4, k2, k2) == (False, "batch-or-heads-mismatch")
+            assert self.elig(q, q, q[:, :2]) == (False, "batch-or-heads-mismatch")
             kk = torch.zeros(1, 4, 96, 64, dtype=torch.float16)
             assert self.elig(q, kk, kk, causal=True) == (False, "causal-cross-length")
+        finally:
+            sdpa.uninstall()
+
+    def test_fp32_under_autograd_stays_stock(self):
+        # the HIP backward takes bf16/fp16 only: fp32 calls whose inputs need
+        # gradients go to stock SDPA, 16-bit ones keep the kernel
+        assert sdpa.install()
+        try:
+            q = torch.zeros(1, 2, 1024, 64, dtype=torch.float32, requires_grad=True)
+            assert self.elig(q, q, q) == (False, "grad-fp32")
+            with torch.no_grad():
+                assert self.elig(q, q, q) == (True, "fast-tier")
+            assert self.elig(q.detach(), q.detach(), q.detach()) == (True, "fast-tier")
+            h = torch.zeros(1, 2, 1024, 64, dtype=torch.bfloat16, requires_grad=True)
+            assert self.elig(h, h, h) == (True, "fast-tier")
         finally:
             sdpa.uninstall()
 
@@ -239,6 +260,21 @@ class TestSdpaOnGpu:
             err = (out.float().cpu() - ref).abs().max().item()
             bar = 1e-5 if dtype == torch.float32 else 4e-3 * ref.abs().max().item()
             assert err <= bar, f"D={d} Dv={dv} causal={causal}: err {err:.3e} > {bar:.3e}"
+
+    def test_fp32_gradients_flow_through_the_patch(self, patched):
+        # fp32 training through the patched op: stock SDPA serves it and the
+        # gradients match stock's; bf16 gradients come from the HIP backward
+        g = torch.Generator().manual_seed(5)
+        base = [torch.randn(1, 2, 1024, 64, generator=g) for _ in range(3)]
+        q, k, v = (x.to("cuda").requires_grad_(True) for x in base)
+        F.scaled_dot_product_attention(q, k, v).sum().backward()
+        q2, k2, v2 = (x.to("cuda").requires_grad_(True) for x in base)
+        patched._orig(q2, k2, v2).sum().backward()
+        for a, b in ((q, q2), (k, k2), (v, v2)):
+            assert torch.equal(a.grad, b.grad)
+        qh, kh, vh = (x.to("cuda", torch.bfloat16).requires_grad_(True) for x in base)
+        F.scaled_dot_product_attention(qh, kh, vh).float().sum().backward()
+        assert all(t.grad is not None and torch.isfinite(t.grad.float()).all() for t in (qh, kh, vh))
 
     def test_uneven_value_head_dim_with_mask_stays_stock(self, patched):
         q, k, _ = self.make(1, 2, 64, 64, 64)

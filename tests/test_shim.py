@@ -15,12 +15,16 @@ import subprocess
 import sys
 import textwrap
 
+import pytest
+
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def run_py(code, env_extra=None, pythonpath=None):
+def run_py(code, env_extra=None, pythonpath=None, shim_mode="force"):
     env = os.environ.copy()
-    env["MTLFLASHATTN_SHIM"] = "force"
+    env.pop("MTLFLASHATTN_SHIM", None)
+    if shim_mode is not None:
+        env["MTLFLASHATTN_SHIM"] = shim_mode
     env["PYTHONPATH"] = os.pathsep.join([p for p in (pythonpath, REPO) if p])
     env.update(env_extra or {})
     return subprocess.run([sys.executable, "-c", textwrap.dedent(code)], capture_output=True, text=True, env=env,
@@ -143,3 +147,30 @@ def test_shimmed_call_reaches_the_contract():
     """)
     assert r.returncode == 0, r.stderr
     assert r.stdout.strip() == "NIE"
+
+
+@pytest.mark.gpu
+def test_default_mode_serves_flash_attn_on_the_gpu(tmp_path):
+    """MTLFLASHATTN_SHIM unset (auto mode) on the MI355X: the .pth-activated
+    finder serves flash_attn.flash_attn_interface, and a bf16 call through it
+    runs the HIP kernel and matches the oracle (_mtlflashattn_finder.py:29-54;
+    the reference's tests/test_shim.py:18-56)."""
+    r = run_py(site_prelude(tmp_path) + textwrap.dedent("""
+        import torch
+        from flash_attn.flash_attn_interface import flash_attn_func
+        import flash_attn, mtlflashattn_amd
+        from oracle import chunked
+        assert flash_attn.__version__ == "2.7.4"
+        assert flash_attn_func is mtlflashattn_amd.flash_attn_func
+        g = torch.Generator().manual_seed(11)
+        q, k, v = (torch.randn(2, 256, 4, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+        out = flash_attn_func(q.cuda(), k.cuda(), v.cuda(), causal=True)
+        torch.cuda.synchronize()
+        ref = chunked.flash_attn_func(q, k, v, causal=True)
+        err = (out.float().cpu() - ref).abs().max().item()
+        assert out.dtype == torch.bfloat16 and err <= 4e-3 * ref.abs().max().item(), err
+        assert "libmtlfa_hip.so" in open("/proc/self/maps").read(), "HIP library not loaded"
+        print("ok", err)
+    """), shim_mode=None)
+    assert r.returncode == 0, r.stderr[-3000:]
+    assert r.stdout.strip().startswith("ok"), r.stdout
