@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MFA_ABI_VERSION 5
+#define MFA_ABI_VERSION 6
 
 /* element types (dtype_in / dtype_out) */
 #define MFA_DTYPE_F16 0
@@ -215,6 +215,27 @@ int32_t mfa_fwd_split_keys(const mfa_fwd_params* params);
 int64_t mfa_fwd_workspace_bytes(const mfa_fwd_params* params, int32_t split_keys);
 int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* workspace, int64_t workspace_bytes,
                     void* stream);
+
+/* Size of the static scratch array behind mfa_fwd_splitkv_static (64 MiB per
+ * GPU, held from the library's first use on that GPU until the process
+ * ends). */
+#define MFA_STATIC_SCRATCH_BYTES (64LL << 20)
+
+/* mfa_fwd_splitkv without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split-KV partials go to a file-scope device array of
+ * MFA_STATIC_SCRATCH_BYTES bytes (one per GPU); a call whose
+ * mfa_fwd_workspace_bytes exceeds that returns MFA_ERR_INVALID with a
+ * message.  Allocates nothing (no hipMalloc, hipFree or allocating library
+ * call); the first call on a GPU looks up the array's device address once.
+ * Same kernels, chunks and results as mfa_fwd_splitkv (bit for bit);
+ * split_keys 0 behaves as mfa_fwd.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, or host threads
+ * without ordering between them) race and must be serialised by the caller;
+ * calls in one stream are ordered and safe.  The array keeps the last call's
+ * partials; nothing needs clearing (each call writes every partial it reads). */
+int mfa_fwd_splitkv_static(const mfa_fwd_params* params, int32_t split_keys, void* stream);
 
 /*
  * Backward pass (gradients of q, k, v).  No counterpart in the reference,

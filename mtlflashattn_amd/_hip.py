@@ -21,7 +21,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime first)
 
 from ._build import LIB_PATH
 
-MFA_ABI_VERSION = 5
+MFA_ABI_VERSION = 6
 MFA_DTYPE_F16 = 0
 MFA_DTYPE_BF16 = 1
 MFA_DTYPE_F32 = 2
@@ -138,6 +138,8 @@ def load():
         lib.mfa_fwd_workspace_bytes.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32]
         lib.mfa_fwd_splitkv.restype = ctypes.c_int
         lib.mfa_fwd_splitkv.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32, _c_ptr, ctypes.c_int64, _c_ptr]
+        lib.mfa_fwd_splitkv_static.restype = ctypes.c_int
+        lib.mfa_fwd_splitkv_static.argtypes = [ctypes.POINTER(MfaFwdParams), _c_i32, _c_ptr]
         lib.mfa_bwd_params_size.restype = ctypes.c_int
         lib.mfa_bwd_params_size.argtypes = []
         lib.mfa_bwd_supported.restype = ctypes.c_int
@@ -203,6 +205,15 @@ def fwd_splitkv(params: MfaFwdParams, chunk: int, workspace: int, workspace_byte
                              _c_ptr(stream))
     if rc != MFA_OK:
         raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_fwd_splitkv failed ({rc})")
+
+
+def fwd_splitkv_static(params: MfaFwdParams, chunk: int, stream: int) -> None:
+    """mfa_fwd_splitkv with the library's static per-GPU scratch as workspace
+    (allocates nothing; calls that overlap on one GPU race)."""
+    lib = load()
+    rc = lib.mfa_fwd_splitkv_static(ctypes.byref(params), int(chunk), _c_ptr(stream))
+    if rc != MFA_OK:
+        raise HipLibraryError(lib.mfa_last_error().decode(errors="replace") or f"mfa_fwd_splitkv_static failed ({rc})")
 
 
 def bwd_workspace_bytes(params: MfaBwdParams) -> int:

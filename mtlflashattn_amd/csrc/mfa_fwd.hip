@@ -45,6 +45,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1841,6 +1842,71 @@ int auto_split_keys(const mfa_fwd_params* p) {
     return kSplitKeys;
 }
 
+// Enqueue a planned split-KV call with its workspace `ws` (plan.ws_bytes
+// bytes, 256-byte aligned): the chunk kernel writes every partial the merge
+// kernel reads (each chunk of each row that exists, lse -inf and O 0 for a
+// chunk without a valid key), so the workspace needs no clearing.
+int launch_splitkv(Plan& plan, void* ws, hipStream_t st, const char* who) {
+    KArgs& a = plan.args;
+    // (the planned rows: a packed grouped-query decode has a.Lq = query heads
+    // per K/V head rows per unit, not the caller's seqlen_q)
+    const int64_t rows = (int64_t)a.nsplit * a.U * a.Lq;
+    a.ws_o = static_cast<float*>(ws);
+    a.ws_lse = a.ws_o + rows * a.ws_ld;
+    // one chunk (every key range fits): the kernel stores O itself
+    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, st, a);
+    if (a.nsplit > 1)
+        hipLaunchKernelGGL(plan.combine, dim3((unsigned)((int64_t)a.U * a.Lq)), dim3(64), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+    return MFA_OK;
+}
+
+}  // namespace
+
+// Workspace of mfa_fwd_splitkv_static: one array per GPU (each device that
+// loads the library's code object gets its own copy, held until the process
+// ends).  In host code `scratch` only names the symbol; its device address on
+// a device comes from hipGetSymbolAddress with that device current, looked up
+// once per device and kept in g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[MFA_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 256;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the device `st` belongs to (the current
+// device for the null stream); the first call on a device looks it up with
+// that device current.
+int static_scratch(hipStream_t st, void** out) {
+    int dev = -1;
+    hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd_splitkv_static: no device for the stream: %s",
+                                        hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv_static: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        void* ptr = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur >= 0 && cur != dev) {
+            const hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess || !ptr)
+            return set_err(MFA_ERR_LAUNCH, "mfa_fwd_splitkv_static: hipGetSymbolAddress(scratch) on device %d: %s",
+                           dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MFA_OK;
+}
+
 }  // namespace
 
 char* mfa_error_buffer() { return g_err; }
@@ -1898,20 +1964,26 @@ int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* work
     if (workspace_bytes < plan.ws_bytes)
         return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: workspace of %lld bytes, %lld needed",
                        (long long)workspace_bytes, (long long)plan.ws_bytes);
-    KArgs& a = plan.args;
-    // (the planned rows: a packed grouped-query decode has a.Lq = query heads
-    // per K/V head rows per unit, not the caller's seqlen_q)
-    const int64_t rows = (int64_t)a.nsplit * a.U * a.Lq;
-    a.ws_o = static_cast<float*>(workspace);
-    a.ws_lse = a.ws_o + rows * a.ws_ld;
+    return launch_splitkv(plan, workspace, static_cast<hipStream_t>(stream), "mfa_fwd_splitkv");
+}
+
+int mfa_fwd_splitkv_static(const mfa_fwd_params* params, int32_t split_keys, void* stream) {
+    g_err[0] = 0;
+    if (split_keys == 0) return mfa_fwd(params, stream);
+    Plan plan;
+    const int rc = make_plan(params, &plan, split_keys);
+    if (rc != MFA_OK) return rc;
+    if (plan.empty) return MFA_OK;
+    if (plan.ws_bytes > MFA_STATIC_SCRATCH_BYTES)
+        return set_err(MFA_ERR_INVALID,
+                       "mfa_fwd_splitkv_static: this call needs %lld bytes of workspace, more than the static "
+                       "scratch's %lld; use mfa_fwd_splitkv with a caller workspace, or larger chunks",
+                       (long long)plan.ws_bytes, (long long)MFA_STATIC_SCRATCH_BYTES);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    // one chunk (every key range fits): the kernel stores O itself
-    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, st, a);
-    if (a.nsplit > 1)
-        hipLaunchKernelGGL(plan.combine, dim3((unsigned)((int64_t)a.U * a.Lq)), dim3(64), 0, st, a);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd_splitkv: launch failed: %s", hipGetErrorString(e));
-    return MFA_OK;
+    void* ws = nullptr;
+    const int src = static_scratch(st, &ws);
+    if (src != MFA_OK) return src;
+    return launch_splitkv(plan, ws, st, "mfa_fwd_splitkv_static");
 }
 
 int mfa_fwd(const mfa_fwd_params* params, void* stream) {
