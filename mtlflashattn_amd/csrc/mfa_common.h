@@ -95,10 +95,16 @@ __device__ const int32_t kNoPages[1] = {0};
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Larger of a and b for scores that are never NaN (finite or -inf):
+// IEEE maximum, which needs no NaN-quieting of its inputs (fmaxf's maxnum
+// costs a canonicalising v_max_f32 per operand that is not a fresh
+// arithmetic result, e.g. an MFMA accumulator or a cross-lane value).
+__device__ __forceinline__ float fmax_nn(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // value of `x` in lane (lane ^ 32) and in this lane, combined by max
 __device__ __forceinline__ float max_halves(float x) {
     auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-    return fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
+    return fmax_nn(__int_as_float(sw[0]), __int_as_float(sw[1]));
 }
 __device__ __forceinline__ float sum_halves(float x) {
     auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);

@@ -93,6 +93,10 @@ constexpr int kWaves = 4;
 #ifndef MFA_PP_PRIO
 #define MFA_PP_PRIO 1
 #endif
+// ping-pong kernel: group 1 issues its K/V loads in its MFMA phase
+#ifndef MFA_PP_DMA_A
+#define MFA_PP_DMA_A 1
+#endif
 // software-pipelined unmasked blocks (QB >= 2)
 #ifndef MFA_PIPELINE
 #define MFA_PIPELINE 1
@@ -177,10 +181,11 @@ __device__ __forceinline__ float qb_max(const f32x16_t (&s)[NKB]) {
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
-            m0 = fmaxf(m0, s[kb][r]);
-            m1 = fmaxf(m1, s[kb][r + 1]);
+            if (kb == 0 && r == 0) continue;
+            m0 = fmax_nn(m0, s[kb][r]);
+            m1 = fmax_nn(m1, s[kb][r + 1]);
         }
-    return max_halves(fmaxf(m0, m1));
+    return max_halves(fmax_nn(m0, m1));
 }
 
 // Running-max update from the block max mx.  The reference max of the wave
@@ -197,7 +202,7 @@ __device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float
     const bool moved = __any((mx - rs.m) * c > tau);
     alpha = 1.f;
     if (moved) {
-        const float mn = fmaxf(rs.m, mx);
+        const float mn = fmax_nn(rs.m, mx);
         alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
         rs.m = mn;
         rs.l *= alpha;
@@ -213,12 +218,27 @@ __device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float
 __device__ __forceinline__ bool qb_update_flat(RowState& rs, float mx, float c, float& mu, float& alpha,
                                                float tau = (float)MFA_RESCALE_TAU) {
     const bool moved = __any((mx - rs.m) * c > tau);
-    const float mn = fmaxf(rs.m, mx);
+    const float mn = fmax_nn(rs.m, mx);
     alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
     rs.m = moved ? mn : rs.m;
     rs.l *= moved ? alpha : 1.f;
     mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
     return moved;
+}
+
+// qb_update without the rescale: the reference moves exactly as in qb_update
+// (m_old keeps the previous running max, for alpha = exp2((m_old - m) * c),
+// which the caller computes, with the rescale of O and l, only when moved)
+__device__ __forceinline__ bool qb_move(RowState& rs, float mx, float c, float& mu, float& m_old,
+                                        float tau = (float)MFA_RESCALE_TAU) {
+    const bool moved = __any((mx - rs.m) * c > tau);
+    m_old = rs.m;
+    rs.m = moved ? fmax_nn(rs.m, mx) : rs.m;
+    mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
+    return moved;
+}
+__device__ __forceinline__ float move_alpha(float m_old, float m_new, float c) {
+    return m_new == -INFINITY ? 1.f : fast_exp2((m_old - m_new) * c);
 }
 
 template <int DB>
@@ -251,10 +271,12 @@ __device__ __forceinline__ uint32_t pack_and_sum(float p0, float p1, float& acc)
 
 // P^T B operands straight from the accumulators: pw[kb][st] holds
 // accumulator registers 8*st..8*st+7 of key block kb.
+// (the block's row sum starts from zero in two independent chains and is
+// added to l at the end, so the sums do not wait for l's rescale)
 template <int NKB, bool IS_BF16>
 __device__ __forceinline__ void qb_probs16(const f32x16_t (&s)[NKB], u32x4_t (&pw)[NKB][2], float& l, float mu,
                                            float c) {
-    float acc[2] = {l, 0.f};  // two independent sum chains
+    float acc[2] = {0.f, 0.f};  // two independent sum chains
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -265,7 +287,7 @@ __device__ __forceinline__ void qb_probs16(const f32x16_t (&s)[NKB], u32x4_t (&p
                 const float p1 = fast_exp2(fmaf(s[kb][8 * st + 2 * w + 1], c, -mu));
                 pw[kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, acc[w & 1]);
             }
-    l = acc[0] + acc[1];
+    l += acc[0] + acc[1];
 }
 
 template <int NKB>
@@ -288,13 +310,15 @@ __device__ __forceinline__ void qb_probs32(f32x16_t (&s)[NKB], float& l, float m
 // probabilities were exp2(x*c - mu), l their sum), -inf for a row with no
 // valid key.
 constexpr float kLn2 = 0.6931471805599453f;
+// lsum[qb]: the row sum of query block qb for this lane's query (both halves)
 template <int QB, int DB, bool IS_BF16>
-__device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32x16_t (&o)[QB][DB],
-                                          const RowState (&rs)[QB], int qrow0, int lane, float c) {
+__device__ __forceinline__ void store_out_l(const KArgs& a, const SeqView& sv, f32x16_t (&o)[QB][DB],
+                                            const RowState (&rs)[QB], const float (&lsum)[QB], int qrow0, int lane,
+                                            float c) {
     const int l32 = lane & 31, half = lane >> 5;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        const float l = sum_halves(rs[qb].l);
+        const float l = lsum[qb];
         const float inv = l > 0.f ? 1.f / l : 0.f;  // fully masked rows -> 0 (_kernel.py:85)
         const int qrow = qrow0 + 32 * qb + l32;
         if (qrow >= sv.Lq) continue;
@@ -325,6 +349,16 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
             }
     }
 }
+// row sums kept per half-wave in rs[qb].l
+template <int QB, int DB, bool IS_BF16>
+__device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32x16_t (&o)[QB][DB],
+                                          const RowState (&rs)[QB], int qrow0, int lane, float c) {
+    float lsum[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) lsum[qb] = sum_halves(rs[qb].l);
+    store_out_l<QB, DB, IS_BF16>(a, sv, o, rs, lsum, qrow0, lane, c);
+}
+
 
 // Split-KV partial of one chunk: O normalised by the chunk's own row sum and
 // the chunk's log2-sum-exp lse = mu + log2(l) (probabilities were
@@ -710,12 +744,11 @@ mfa_fwd16_kernel(KArgs a) {
                 if (ci < NKB) {  // partial row max over key block ci
 #pragma unroll
                     for (int r = 0; r < 16; r += 2) {
-                        mpart[0] = fmaxf(mpart[0], sacc[qb][ci][r]);
-                        mpart[1] = fmaxf(mpart[1], sacc[qb][ci][r + 1]);
+                        mpart[0] = fmax_nn(mpart[0], sacc[qb][ci][r]);
+                        mpart[1] = fmax_nn(mpart[1], sacc[qb][ci][r + 1]);
                     }
                 } else if (ci == NKB) {  // merge halves, new running max
-                    moved = qb_update(rs[qb], max_halves(fmaxf(mpart[0], mpart[1])), c, mu, alpha, tau);
-                    lacc[0] = rs[qb].l;
+                    moved = qb_update(rs[qb], max_halves(fmax_nn(mpart[0], mpart[1])), c, mu, alpha, tau);
                 } else if (ci < NKB + 1 + DB) {  // rescale O rows (only if some row's max moved)
                     const int db = ci - NKB - 1;
                     if (moved) {
@@ -730,7 +763,8 @@ mfa_fwd16_kernel(KArgs a) {
                         const float p1 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w + 1], c, -mu));
                         pw[qb][kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, lacc[w & 1]);
                     }
-                    if (ci == NCH - 1) rs[qb].l = lacc[0] + lacc[1];
+                    // (the block's sum joins l at the end, as in qb_probs16)
+                    if (ci == NCH - 1) rs[qb].l += lacc[0] + lacc[1];
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -1099,6 +1133,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
                     o[qb][db] = mfma16(f, __builtin_bit_cast(op_t, pw[qb][kb][st]), o[qb][db]);
+
             } else {
                 const op_t f = kfr[i % (AH + 1)];
                 constexpr int m = i - NPV, kb = m % NKB, s = m / NKB;
@@ -1137,17 +1172,27 @@ mfa_fwd16_pp_kernel(KArgs a) {
         // both query blocks' max, update and probabilities in one branch-free
         // stretch (independent chains for the scheduler to interleave); the
         // rare rescale of O follows (O is next read by PV in the next phase)
-        float mx[QB], mu[QB], alpha[QB];
+        float mx[QB], mu[QB], m_old[QB], bsum[QB];
         bool moved[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) mx[qb] = qb_max<NKB>(sacc[qb]);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_update_flat(rs[qb], mx[qb], c, mu[qb], alpha[qb], tau);
+        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_move(rs[qb], mx[qb], c, mu[qb], m_old[qb], tau);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu[qb], c);
+        for (int qb = 0; qb < QB; ++qb) {
+            bsum[qb] = 0.f;
+            qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], bsum[qb], mu[qb], c);
+        }
+        // the rare rescale of O and l: alpha only when the reference moved
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
-            if (moved[qb]) scale_rows<DB>(o[qb], alpha[qb]);
+            if (moved[qb]) {
+                const float alpha = move_alpha(m_old[qb], rs[qb].m, c);
+                scale_rows<DB>(o[qb], alpha);
+                rs[qb].l *= alpha;
+            }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) rs[qb].l += bsum[qb];
         // (the row sums stay in this phase too)
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) pin(rs[qb].l);
@@ -1183,21 +1228,30 @@ mfa_fwd16_pp_kernel(KArgs a) {
     };
     using EVEN = std::true_type;
     using ODD = std::false_type;
+    // With MFA_PP_DMA_A, group 1 issues its share of batch u at the start of
+    // its own A(u) (phase 2u+1) instead of in its softmax phase B(u-1), where
+    // the load issue sat on the critical path (the phase pairs A of group 0
+    // with B of group 1).  Batch u is first read at phase 2u+4 and overwrites
+    // stages last read at phase 2u-1, so issuing it at 2u+1 is safe; group 1
+    // then keeps at most its newest batch in flight at every barrier.
     auto run = [&](auto grp_c) __attribute__((always_inline)) {
         constexpr int G = decltype(grp_c)::value;
+        // (head dims up to 64 only: at 128 a block's loads need the extra phase)
+        constexpr bool LATE = MFA_PP_DMA_A && G == 1 && DP <= 64;
         if constexpr (G == 1) {
-            dma(0);
-            phase_sync(EVEN{});  // phase 0 (idle)
+            if constexpr (!LATE) dma(0);
+            phase_sync(std::integral_constant<bool, !LATE>{});  // phase 0 (idle)
         }
         for (int u = 0; u < nblk; ++u) {
-            if constexpr (G == 0) dma(u);
+            if constexpr (G == 0 || LATE) dma(u);
             phase_a(u);
             if constexpr (G == 0) phase_sync(EVEN{}); else phase_sync(ODD{});
-            if constexpr (G == 1) dma(u + 1);
+            if constexpr (G == 1 && !LATE) dma(u + 1);
             phase_b(u);
-            if constexpr (G == 0) phase_sync(ODD{}); else phase_sync(EVEN{});
+            if constexpr (G == 0) phase_sync(ODD{});
+            else phase_sync(std::integral_constant<bool, !LATE>{});
         }
-        if constexpr (G == 0) dma(nblk);
+        if constexpr (G == 0 || LATE) dma(nblk);
         phase_a(nblk);
         if constexpr (G == 0) {
             phase_sync(EVEN{});  // phase 2n
