@@ -63,6 +63,7 @@ struct KArgs {
     int32_t U;        // (sequence, head) units = B * Hq
     int32_t upx;      // units per XCD (grouped schedule)
     int32_t grouped;  // 1: XCD-grouped by K/V head, 0: linear
+    int32_t xcd_shift;  // log2 of the device's XCD count (grouped schedule)
     int32_t tile_major;  // grouped order within an XCD: 1 tile-major, 0 unit-major
     // split-KV: the key range of a sequence is cut into chunks of split_keys
     // keys (a multiple of the key block); workgroup (tile, split) writes the
@@ -184,16 +185,17 @@ __device__ __forceinline__ int vt_pos(int kk) {
 __device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int& hq, int& t) {
     int unit, tt;
     if (a.grouped) {
-        // workgroup ids are dealt round-robin over the 8 XCDs; XCD x owns the
-        // K/V head groups g = b*Hkv + hkv with g % 8 == x, all their q heads
+        // workgroup ids are dealt round-robin over the X = 2^xcd_shift XCDs
+        // (8 on MI355X); XCD x owns the
+        // K/V head groups g = b*Hkv + hkv with g % X == x, all their q heads
         // and all their tiles.  Within an XCD the order is unit-major (all
         // tiles of one (sequence, q head), heaviest first, then the next), so
         // the workgroups resident on the XCD share one head's K/V in its L2,
         // when every tile costs the same; when tiles differ (causal, windows)
         // it is tile-major (the heaviest tiles of every unit first), so the
         // XCD's CUs take the work longest first and finish together.
-        const int xcd = bid & 7;
-        const int slot = bid >> 3;
+        const int xcd = bid & ((1 << a.xcd_shift) - 1);
+        const int slot = bid >> a.xcd_shift;
         int j;
         if (a.tile_major) {
             tt = slot / a.upx;
@@ -204,7 +206,7 @@ __device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int
         }
         const int R = a.Hq / a.Hkv;
         const int jg = j / R;
-        const int g = xcd + 8 * jg;
+        const int g = xcd + (jg << a.xcd_shift);
         const int r = j - jg * R;
         b = g / a.Hkv;
         const int hkv = g - b * a.Hkv;

@@ -43,6 +43,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -1568,7 +1569,6 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // (the two tile heights' measured non-causal rates differ by 9%).  When the
 // 512-row tiles all run at once the heaviest sets the time, and 256-row
 // tiles, paired heavy with light on each CU, nearly halve it.
-constexpr int kChipCUs = 256;
 int64_t host_key_lo(const mfa_fwd_params* p, int64_t c) {
     return p->window_left >= 0 ? std::max<int64_t>(c - p->window_left, 0) : 0;
 }
@@ -1578,7 +1578,7 @@ int64_t host_key_hi(const mfa_fwd_params* p, int64_t c) {
     if (p->window_right >= 0) hi = std::min<int64_t>(hi, c + p->window_right);
     return hi;
 }
-double tile_makespan(const mfa_fwd_params* p, int rows, double block_cost) {
+double tile_makespan(const mfa_fwd_params* p, int rows, double block_cost, int cus) {
     const int64_t dq = (int64_t)p->seqlen_k - p->seqlen_q;
     const int64_t T = (p->seqlen_q + rows - 1) / rows;
     int64_t heaviest = 0, total = 0;
@@ -1590,15 +1590,74 @@ double tile_makespan(const mfa_fwd_params* p, int rows, double block_cost) {
         total += n;
     }
     const double units = (double)p->batch * p->heads_q;
-    return std::max((double)heaviest, units * (double)total / kChipCUs) * block_cost;
+    return std::max((double)heaviest, units * (double)total / cus) * block_cost;
 }
-bool prefer_pp256(const mfa_fwd_params* p) {
+bool prefer_pp256(const mfa_fwd_params* p, int cus) {
     if (p->cu_seqlens_q || (!p->causal && p->window_left < 0 && p->window_right < 0)) return false;
     if (p->seqlen_q > (1 << 20)) return false;  // (bounds the estimate's loop; long rows balance anyway)
-    return tile_makespan(p, 256, 0.545) < 0.9 * tile_makespan(p, 512, 1.0);
+    return tile_makespan(p, 256, 0.545, cus) < 0.9 * tile_makespan(p, 512, 1.0, cus);
 }
 
-int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
+// ---- Chip geometry: compute units and XCDs of the device a call runs on,
+// looked up once per device (hipDeviceGetAttribute with the device current)
+// and kept.  The tile choices compare grids against the CU count, and the
+// grouped schedule deals workgroups over the XCDs.  MI355X: 256 CUs in 8
+// XCDs, also the defaults when no device is visible (planning-only calls on a
+// host without a GPU).  MTLFLASHATTN_CHIP_CUS / MTLFLASHATTN_CHIP_XCDS
+// override the values (tuning and tests).
+struct ChipGeom {
+    int cus = 256;
+    int xcds = 8;
+};
+constexpr int kMaxGeomDevices = 256;
+std::mutex g_geom_mu;
+ChipGeom g_geom[kMaxGeomDevices];
+bool g_geom_known[kMaxGeomDevices];
+
+int env_positive(const char* name) {
+    const char* v = getenv(name);
+    if (!v || !*v) return 0;
+    const long x = strtol(v, nullptr, 10);
+    return x > 0 && x < (1 << 20) ? (int)x : 0;
+}
+
+ChipGeom chip_geometry(int dev) {
+    ChipGeom g;
+    if (dev < 0 || dev >= kMaxGeomDevices) return g;
+    std::lock_guard<std::mutex> lock(g_geom_mu);
+    if (!g_geom_known[dev]) {
+        int cur = -1, v = 0;
+        if (hipGetDevice(&cur) == hipSuccess) {
+            const bool switch_dev = cur != dev && hipSetDevice(dev) == hipSuccess;
+            if ((switch_dev || cur == dev) &&
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+                g.cus = v;
+            if ((switch_dev || cur == dev) &&
+                hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0)
+                g.xcds = v;
+            if (switch_dev) (void)hipSetDevice(cur);
+        }
+        (void)hipGetLastError();  // a failed query leaves no sticky error for the caller
+        if (const int e = env_positive("MTLFLASHATTN_CHIP_CUS")) g.cus = e;
+        if (const int e = env_positive("MTLFLASHATTN_CHIP_XCDS")) g.xcds = e;
+        g_geom[dev] = g;
+        g_geom_known[dev] = true;
+    }
+    return g_geom[dev];
+}
+// geometry of the device `st` belongs to (the current device for the null stream)
+ChipGeom chip_geometry_of(hipStream_t st) {
+    int dev = -1;
+    const hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        dev = 0;
+    }
+    return chip_geometry(dev);
+}
+ChipGeom chip_geometry_current() { return chip_geometry_of(nullptr); }
+
+int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int split_keys = 0) {
     if (!p) return set_err(MFA_ERR_INVALID, "mfa_fwd: params is NULL");
     // Single-row grouped-query decode: the R query heads of a K/V head become
     // the R rows of one sequence (the same q/o memory through other strides),
@@ -1718,10 +1777,10 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
         if (dp == 128)  // and rows long enough: >= 8 tiles per head, 16 when causal (measured:
                         // B=32 Lq=256 44 vs 40 us, B=16 Lq=1024 causal 145 vs 116 on the ping-pong tiles)
             fills_chip = !p->cu_seqlens_q && p->window_left < 0 && p->window_right < 0 &&
-                         units * (rows256 / 256) >= 256 && 4 * rows256 <= 5 * rows128 &&
+                         units * (rows256 / 256) >= geom.cus && 4 * rows256 <= 5 * rows128 &&
                          rows256 / 256 >= (p->causal ? 16 : 8);
         else
-            fills_chip = units * (rows512 / 512) >= 256 && 4 * rows512 <= 5 * rows256;
+            fills_chip = units * (rows512 / 512) >= geom.cus && 4 * rows512 <= 5 * rows256;
     }
     bool pp256 = p->tile_hint == MFA_TILE_PINGPONG256;
     if (split_keys != 0) {
@@ -1747,7 +1806,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     // 83, B=1 L=8192 H=8 188 -> 156).
     if (p->tile_hint == MFA_TILE_AUTO && !fills_chip && !paged && split_keys == 0 && dp <= 64 &&
         din != MFA_DTYPE_F32 && !bias && !p->cu_seqlens_q && p->window_left < 0 && p->window_right < 0 &&
-        units * (rows256 / 256) >= 256 && rows256 / 256 >= 4) {
+        units * (rows256 / 256) >= geom.cus && rows256 / 256 >= 4) {
         // (rows of >= 4 tiles: shorter rows, e.g. B=64 L=256 H=16, run 40 vs
         // 50 us on the 4-wavefront kernel)
         fills_chip = true;
@@ -1770,10 +1829,10 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
         const int64_t t512 = rows512 / 512;
         if (windowed || (p->causal && bias) || p->cu_seqlens_q)
             fills_chip = false;
-        else if (p->causal && t512 <= 8 && units * t512 > 256)
+        else if (p->causal && t512 <= 8 && units * t512 > geom.cus)
             fills_chip = false;
         else
-            pp256 = prefer_pp256(p);
+            pp256 = prefer_pp256(p, geom.cus);
     }
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp, paged) : select32<false>(dp, paged);
@@ -1844,11 +1903,15 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
     a.T = (p->seqlen_q + rows - 1) / rows;
     a.U = p->batch * p->heads_q;
     const int64_t G = (int64_t)p->batch * p->heads_kv;
-    if (G % 8 == 0 && G > 0) {
+    const int X = geom.xcds;
+    int xshift = 0;
+    while ((1 << xshift) < X) ++xshift;
+    if (G > 0 && (1 << xshift) == X && G % X == 0) {  // (a power-of-two XCD count dividing the groups)
         a.grouped = 1;
+        a.xcd_shift = xshift;
         a.tile_major = (p->causal || p->window_left >= 0 || p->window_right >= 0) ? 1 : 0;
-        a.upx = (int32_t)(G / 8) * (p->heads_q / p->heads_kv);
-        plan->grid = 8 * a.upx * a.T;
+        a.upx = (int32_t)(G / X) * (p->heads_q / p->heads_kv);
+        plan->grid = X * a.upx * a.T;
     } else {
         a.grouped = 0;
         a.upx = 0;
@@ -1886,8 +1949,8 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, int split_keys = 0) {
 // single pass: there the split's merge and extra workgroups cost ~8%.
 constexpr int kSplitMaxLq = 256;
 constexpr int kSplitKeys = 2048;
-constexpr int64_t kSplitMaxUnits = 512;
-int auto_split_keys(const mfa_fwd_params* p) {
+int auto_split_keys(const mfa_fwd_params* p, const ChipGeom& geom) {
+    const int64_t kSplitMaxUnits = 2 * (int64_t)geom.cus;  // two workgroups per CU
     if (!p || p->dtype_in == MFA_DTYPE_F32 || p->tile_hint == MFA_TILE_PINGPONG ||
         p->tile_hint == MFA_TILE_PINGPONG256)
         return 0;
@@ -1982,7 +2045,7 @@ int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info) {
     g_err[0] = 0;
     if (!info) return set_err(MFA_ERR_INVALID, "mfa_fwd_launch_info: info is NULL");
     Plan plan;
-    const int rc = make_plan(params, &plan);
+    const int rc = make_plan(params, &plan, chip_geometry_current());
     if (rc != MFA_OK) return rc;
     info->grid_x = plan.empty ? 0 : plan.grid;
     info->block_x = plan.cfg.threads;
@@ -1994,13 +2057,13 @@ int mfa_fwd_launch_info(const mfa_fwd_params* params, mfa_launch_info* info) {
     return MFA_OK;
 }
 
-int32_t mfa_fwd_split_keys(const mfa_fwd_params* params) { return auto_split_keys(params); }
+int32_t mfa_fwd_split_keys(const mfa_fwd_params* params) { return auto_split_keys(params, chip_geometry_current()); }
 
 int64_t mfa_fwd_workspace_bytes(const mfa_fwd_params* params, int32_t split_keys) {
     g_err[0] = 0;
     if (split_keys == 0) return 0;
     Plan plan;
-    const int rc = make_plan(params, &plan, split_keys);
+    const int rc = make_plan(params, &plan, chip_geometry_current(), split_keys);
     if (rc != MFA_OK) return rc;
     return plan.empty ? 0 : plan.ws_bytes;
 }
@@ -2010,7 +2073,7 @@ int mfa_fwd_splitkv(const mfa_fwd_params* params, int32_t split_keys, void* work
     g_err[0] = 0;
     if (split_keys == 0) return mfa_fwd(params, stream);
     Plan plan;
-    const int rc = make_plan(params, &plan, split_keys);
+    const int rc = make_plan(params, &plan, chip_geometry_of(static_cast<hipStream_t>(stream)), split_keys);
     if (rc != MFA_OK) return rc;
     if (plan.empty) return MFA_OK;
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
@@ -2025,7 +2088,7 @@ int mfa_fwd_splitkv_static(const mfa_fwd_params* params, int32_t split_keys, voi
     g_err[0] = 0;
     if (split_keys == 0) return mfa_fwd(params, stream);
     Plan plan;
-    const int rc = make_plan(params, &plan, split_keys);
+    const int rc = make_plan(params, &plan, chip_geometry_of(static_cast<hipStream_t>(stream)), split_keys);
     if (rc != MFA_OK) return rc;
     if (plan.empty) return MFA_OK;
     if (plan.ws_bytes > MFA_STATIC_SCRATCH_BYTES)
@@ -2043,7 +2106,7 @@ int mfa_fwd_splitkv_static(const mfa_fwd_params* params, int32_t split_keys, voi
 int mfa_fwd(const mfa_fwd_params* params, void* stream) {
     g_err[0] = 0;
     Plan plan;
-    const int rc = make_plan(params, &plan);
+    const int rc = make_plan(params, &plan, chip_geometry_of(static_cast<hipStream_t>(stream)));
     if (rc != MFA_OK) return rc;
     if (plan.empty) return MFA_OK;
     hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, static_cast<hipStream_t>(stream), plan.args);

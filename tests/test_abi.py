@@ -14,6 +14,8 @@ import torch
 
 from mtlflashattn_amd import _build, _hip, _kernel
 
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "mfa.h")
 
 
@@ -281,3 +283,41 @@ def test_split_kv_rejects_a_small_or_misaligned_workspace(lib):
         _hip.MFA_ERR_INVALID
     assert b"aligned" in lib.mfa_last_error()
     assert lib.mfa_fwd_splitkv(ctypes.byref(p), 1024, None, need, None) == _hip.MFA_ERR_INVALID
+
+
+def test_plan_uses_the_device_geometry():
+    """Tile and split-KV choices compare grids against the device's CU count
+    (queried per device; MI355X 256 CUs / 8 XCDs by default, the env override
+    stands in for a partitioned device here).  On a 32-CU, 1-XCD part a
+    B=1 L=2048 H=16 D=64 call fills the chip with 512-row ping-pong tiles,
+    which on 256 CUs would leave CUs idle (4-wavefront kernel there), and a
+    B=4 Hq=32 decode already fills it without split-KV."""
+    import subprocess
+    import sys
+    import textwrap
+
+    code = textwrap.dedent("""
+        import torch
+        from mtlflashattn_amd import _hip, _kernel
+        q = torch.empty(1, 2048, 16, 64, dtype=torch.bfloat16)
+        print(_kernel.launch_info(q, q, q).kernel_name.decode())
+        p = _hip.MfaFwdParams()
+        p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k = 4, 32, 32, 1, 8192
+        p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[torch.bfloat16]
+        print(_hip.split_keys(p))
+    """)
+    out = {}
+    for cus, xcds in ((None, None), (32, 1)):
+        env = dict(os.environ)
+        env.pop("MTLFLASHATTN_CHIP_CUS", None)
+        env.pop("MTLFLASHATTN_CHIP_XCDS", None)
+        if cus:
+            env["MTLFLASHATTN_CHIP_CUS"], env["MTLFLASHATTN_CHIP_XCDS"] = str(cus), str(xcds)
+        env["PYTHONPATH"] = REPO
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        out[cus] = r.stdout.strip().splitlines()
+    if torch.cuda.is_available():
+        pytest.skip("the default leg assumes 256 CUs; a visible device reports its own")
+    assert out[None][0].startswith("mfa_fwd16<bf16,d64") and out[None][1] == "2048"
+    assert out[32][0].startswith("mfa_fwd16pp<bf16,d64,2,2>") and out[32][1] == "0"

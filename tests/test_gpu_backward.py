@@ -266,3 +266,22 @@ def test_varlen_with_empty_key_sequences_and_lse_gradient():
         ref[2][c:d] += gi[2][0]
     check_grads((qg.grad, kg.grad, vg.grad), ref, torch.float16, "varlen + lse gradient", factor=2.0)
     assert torch.count_nonzero(qg.grad[:3]) == 0
+
+
+def test_long_rows_config3_shape():
+    """Gradients at config 3's full shape (fp16, B=1, L=8192, H=16, D=128,
+    causal; inputs from seed 2): every head runs on the kernels, and the full
+    dq/dk/dv of heads 0 and 15 (8192-key rows, long causal tails) are checked
+    against the oracle's autograd."""
+    q, k, v = make_qkv(1, 8192, 8192, 16, 16, 128, torch.float16, seed=2)
+    g = torch.Generator().manual_seed(3)
+    dout = torch.randn(q.shape, generator=g).to(DEV, torch.float16)
+    dq, dk, dv = fp32_grads(q, k, v, dout, default_scale(128), causal=True)
+    torch.cuda.synchronize()
+    for h in (0, 15):
+        sl = slice(h, h + 1)
+        ref = chunked.attention_grads(q[:, :, sl], k[:, :, sl], v[:, :, sl], dout[:, :, sl], causal=True)
+        got = (dq[:, :, sl], dk[:, :, sl], dv[:, :, sl])
+        errs = [rel_err(a, b) for a, b in zip(got, ref)]
+        print(f"config3 shape head {h}: dq {errs[0]:.2e} dk {errs[1]:.2e} dv {errs[2]:.2e} (x max|ref|)")
+        check_grads(got, ref, torch.float16, f"config3 shape head {h}")

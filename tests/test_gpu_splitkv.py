@@ -4,14 +4,14 @@ sizes are forced so that short test shapes run through many chunks, including
 empty ones (causal, window, varlen tails) and chunks whose every row is masked.
 
 Bar: the bf16/fp16 bars of the single-pass kernels (fp32 output <=
-2e-3*max|ref|, 16-bit output <= 4e-3*max|ref|).  On long key ranges with few
-query rows, O averages over many keys, max|ref| shrinks like 1/sqrt(keys) while
-the rounding of each probability to 16 bits does not, and the single-pass
-kernel itself can exceed that bar; there the split result must stay within
-1.25x of the single-pass kernel's own error on the same inputs (both errors are
-measured against the oracle).  The bit-exact properties hold within split-KV
-too: GQA equals repeated K/V, each varlen sequence equals its dense B=1 call,
-and a single chunk reproduces the single-pass result."""
+2e-3*max|ref|, 16-bit output <= 4e-3*max|ref|), for the split result and for
+the single-pass result on the same inputs alike.  Shapes measured above the
+fp32-output bar are listed in OVER_BAR with their allowance: single query rows
+over thousands of keys, where O averages over many keys and max|ref| shrinks
+while the rounding of each probability to 16 bits does not (the error is that
+of the 16-bit P, single pass and split alike).  The bit-exact properties hold
+within split-KV too: GQA equals repeated K/V, each varlen sequence equals its
+dense B=1 call, and a single chunk reproduces the single-pass result."""
 from __future__ import annotations
 
 import pytest
@@ -25,6 +25,14 @@ from gpu_util import REL_16, REL_16_OUT, default_scale, make_qkv, make_varlen, m
 pytestmark = pytest.mark.gpu
 
 DTYPES16 = [torch.bfloat16, torch.float16]
+
+# fp32-output error / max|ref| allowed for the shapes measured above 2e-3 on
+# MI355X (measured ratio in the comment; single pass and split both checked):
+# one query row, Lk = 4096, Hq = 8, Hkv = 2, D = 128, bf16, 2048-key chunks.
+OVER_BAR = {
+    ("auto split decode", torch.bfloat16): 2.6e-3,         # split 2.31e-3, single 1.94e-3
+    ("auto split decode causal", torch.bfloat16): 2.6e-3,  # the same rows (one row sees every key)
+}
 
 
 @pytest.fixture
@@ -58,11 +66,13 @@ def check(q, k, v, what="", **kw):
     finally:
         _kernel._SPLIT_KEYS = saved
     ref_max = ref.abs().max().item()
-    for got, base, bar, kind in ((out32, single32, REL_16 * ref_max, "fp32 out"),
+    rel32 = OVER_BAR.get((what, q.dtype), REL_16)
+    for got, base, bar, kind in ((out32, single32, rel32 * ref_max, "fp32 out"),
                                  (out, single, REL_16_OUT * ref_max, f"{q.dtype} out")):
         err, err_single = max_err(got, ref), max_err(base, ref)
-        assert err <= max(bar, 1.25 * err_single), \
-            f"{what} ({kind}): split err {err:.3e}, single-pass err {err_single:.3e}, bar {bar:.3e}"
+        assert err <= bar and err_single <= bar, \
+            (f"{what} ({kind}): split err {err / ref_max:.3e}, single-pass err {err_single / ref_max:.3e} "
+             f"x max|ref|, bar {bar / ref_max:.3e}")
     return out
 
 
@@ -124,7 +134,8 @@ def test_varlen(chunk, dtype):
     ref_max = ref.abs().max().item()
     for got, base, bar in ((out32, single32, REL_16 * ref_max), (out, single, REL_16_OUT * ref_max)):
         err, err_single = max_err(got, ref), max_err(base, ref)
-        assert err <= max(bar, 1.25 * err_single), f"varlen split err {err:.3e}, single {err_single:.3e}"
+        assert err <= bar and err_single <= bar, \
+            f"varlen split err {err / ref_max:.3e}, single {err_single / ref_max:.3e} x max|ref|"
     # each sequence equals its dense B=1 call bit for bit (same chunks)
     sq = [0] + torch.tensor(lens_q).cumsum(0).tolist()
     sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()

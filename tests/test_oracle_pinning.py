@@ -497,3 +497,67 @@ def test_lse_gradient_matches_finite_differences_and_closed_form():
     p = torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1)
     want = 0.4 * torch.einsum("bhij,bjhd->bihd", p, k)
     close(dq, want, atol=1e-10)
+
+
+def test_varlen_gradients_match_finite_differences_and_sdpa():
+    """oracle.chunked.attention_grads_varlen: a gradcheck (float64) of the
+    packed varlen forward over a ragged batch (an empty query sequence, an
+    empty key sequence, Lq != Lk, grouped-query heads), and per sequence the
+    gradients torch's own SDPA autograd gives (causal rows with Lq == Lk,
+    where SDPA's top-left causal equals bottom-right)."""
+    import torch.nn.functional as F
+
+    g = torch.Generator().manual_seed(31)
+    lens_q, lens_k = [3, 0, 5, 2], [4, 3, 5, 0]
+    Hq, Hkv, D = 4, 2, 8
+    q = torch.randn(sum(lens_q), Hq, D, generator=g, dtype=torch.float64)
+    k = torch.randn(sum(lens_k), Hkv, D, generator=g, dtype=torch.float64)
+    v = torch.randn(sum(lens_k), Hkv, D, generator=g, dtype=torch.float64)
+    cu_q = torch.tensor([0] + lens_q).cumsum(0)
+    cu_k = torch.tensor([0] + lens_k).cumsum(0)
+    dout = torch.randn(q.shape, generator=g, dtype=torch.float64)
+
+    def _varlen_f64(q, k, v):
+        outs = []
+        for i in range(len(lens_q)):
+            a, b, c, d = cu_q[i], cu_q[i + 1], cu_k[i], cu_k[i + 1]
+            if b == a:
+                continue
+            if d == c:
+                outs.append(torch.zeros(b - a, Hq, D, dtype=torch.float64))
+                continue
+            o = chunked.flash_torch(q[None, a:b].transpose(1, 2), k[None, c:d].transpose(1, 2),
+                                    v[None, c:d].transpose(1, 2), 0.3, True, grad=True, dtype=torch.float64)
+            outs.append(o[0].transpose(0, 1))
+        return torch.cat(outs, dim=0)
+
+    assert torch.autograd.gradcheck(_varlen_f64, tuple(t.clone().requires_grad_(True) for t in (q, k, v)))
+    dq, dk, dv = chunked.attention_grads_varlen(q, k, v, dout, cu_q, cu_k, softmax_scale=0.3, causal=True,
+                                                dtype=torch.float64)
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    (_varlen_f64(qa, ka, va) * dout).sum().backward()
+    close(dq, qa.grad, atol=1e-12)
+    close(dk, ka.grad, atol=1e-12)
+    close(dv, va.grad, atol=1e-12)
+    # the one sequence with Lq == Lk (5 x 5) against torch SDPA's autograd
+    a, b, c, d = cu_q[2], cu_q[3], cu_k[2], cu_k[3]
+    qs, ks, vs = (t[None, x:y].transpose(1, 2).clone().requires_grad_(True)
+                  for t, x, y in ((q, a, b), (k, c, d), (v, c, d)))
+    out = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True, scale=0.3, enable_gqa=True)
+    (out * dout[None, a:b].transpose(1, 2)).sum().backward()
+    close(dq[a:b], qs.grad[0].transpose(0, 1), atol=1e-10)
+    close(dk[c:d], ks.grad[0].transpose(0, 1), atol=1e-10)
+    close(dv[c:d], vs.grad[0].transpose(0, 1), atol=1e-10)
+    # sequence 0 (Lq = 3 < Lk = 4): bottom-right causal as an explicit SDPA mask
+    a, b, c, d = cu_q[0], cu_q[1], cu_k[0], cu_k[1]
+    qs, ks, vs = (t[None, x:y].transpose(1, 2).clone().requires_grad_(True)
+                  for t, x, y in ((q, a, b), (k, c, d), (v, c, d)))
+    mask = torch.arange(d - c)[None, :] <= torch.arange(b - a)[:, None] + ((d - c) - (b - a))
+    out = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=mask, scale=0.3, enable_gqa=True)
+    (out * dout[None, a:b].transpose(1, 2)).sum().backward()
+    close(dq[a:b], qs.grad[0].transpose(0, 1), atol=1e-10)
+    close(dk[c:d], ks.grad[0].transpose(0, 1), atol=1e-10)
+    close(dv[c:d], vs.grad[0].transpose(0, 1), atol=1e-10)
+    # sequences without queries or keys get no gradient on their rows
+    assert (dk[cu_k[1]:cu_k[2]] == 0).all() and (dv[cu_k[1]:cu_k[2]] == 0).all()
+    assert (dq[cu_q[3]:cu_q[4]] == 0).all()
