@@ -98,6 +98,13 @@ constexpr int kWaves = 4;
 #ifndef MFA_PP_DMA_A
 #define MFA_PP_DMA_A 1
 #endif
+// ping-pong kernel at head dims up to 64: the row sums of a block's rounded
+// probabilities are issued after all of its probabilities, late in the
+// softmax phase, when the partner wavefront's MFMAs are mostly done (dot2
+// instructions wait while the other wavefront of the SIMD issues MFMAs)
+#ifndef MFA_PP_LATE_SUM
+#define MFA_PP_LATE_SUM 1
+#endif
 // software-pipelined unmasked blocks (QB >= 2)
 #ifndef MFA_PIPELINE
 #define MFA_PIPELINE 1
@@ -122,6 +129,8 @@ struct RowState {
     int lo, hi;  // valid key interval [lo, hi]
     float slope; // ALiBi slope (0 without ALiBi)
     float m;     // running max (raw-score units without BIAS, natural-log units with)
+    float mu;    // exponent offset m*c of the probabilities (0 while m = -inf)
+    float thr;   // m + tau/c: a larger block max moves the reference
     float l;     // running row sum (this half-wave's keys)
 };
 
@@ -190,56 +199,48 @@ __device__ __forceinline__ float qb_max(const f32x16_t (&s)[NKB]) {
 }
 
 // Running-max update from the block max mx.  The reference max of the wave
-// moves (to every row's exact max) only when some row's max grew by more than
-// tau (MFA_RESCALE_TAU) in the exp2 domain; otherwise probabilities are taken
-// against the previous reference, so p <= 2^tau.  O and l always use the same
-// reference, so the final O/l is unaffected.  Returns true when the reference
-// moved (wave-uniform); alpha is then the factor for O and l.  Rows with no
-// valid key so far keep m = -inf and get mu = 0, so masked scores give p = 0.
-// With tau = 0 a row whose max did not grow gets alpha = exp2(0) = 1 exactly,
-// so each row's arithmetic is independent of the other rows of its wave.
-__device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float& mu, float& alpha,
-                                          float tau = (float)MFA_RESCALE_TAU) {
-    const bool moved = __any((mx - rs.m) * c > tau);
-    alpha = 1.f;
-    if (moved) {
-        const float mn = fmax_nn(rs.m, mx);
-        alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
-        rs.m = mn;
-        rs.l *= alpha;
-    }
-    mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
-    return moved;
+// moves (to every row's exact max) only when some row's block max exceeds its
+// threshold thr = m + tau/c, i.e. grew by more than tau (MFA_RESCALE_TAU) in
+// the exp2 domain; otherwise probabilities are taken against the previous
+// reference, so p <= 2^tau.  O and l always use the same reference, so the
+// final O/l is unaffected.  The exponent offset mu = m*c and thr change only
+// on a move, so a block that moves no row costs one compare per row.  Rows
+// with no valid key so far keep m = thr = -inf and mu = 0, so masked scores
+// give p = 0.  With tau = 0 a row whose max did not grow gets
+// alpha = exp2(0) = 1 exactly, so each row's arithmetic is independent of
+// the other rows of its wave.
+__device__ __forceinline__ void row_reset(RowState& rs) {
+    rs.m = -INFINITY;
+    rs.thr = -INFINITY;
+    rs.mu = 0.f;
+    rs.l = 0.f;
 }
-
-// qb_update without a branch: the same result, with the rescale of O left
-// to the caller, by `alpha`, exactly when it returns true.  (alpha is not
-// forced to 1 otherwise, so the caller's conditional rescale cannot be
-// turned into an unconditional multiply by 1.)
-__device__ __forceinline__ bool qb_update_flat(RowState& rs, float mx, float c, float& mu, float& alpha,
-                                               float tau = (float)MFA_RESCALE_TAU) {
-    const bool moved = __any((mx - rs.m) * c > tau);
-    const float mn = fmax_nn(rs.m, mx);
-    alpha = (mn == -INFINITY) ? 1.f : fast_exp2((rs.m - mn) * c);
-    rs.m = moved ? mn : rs.m;
-    rs.l *= moved ? alpha : 1.f;
-    mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
-    return moved;
-}
-
-// qb_update without the rescale: the reference moves exactly as in qb_update
-// (m_old keeps the previous running max, for alpha = exp2((m_old - m) * c),
-// which the caller computes, with the rescale of O and l, only when moved)
-__device__ __forceinline__ bool qb_move(RowState& rs, float mx, float c, float& mu, float& m_old,
-                                        float tau = (float)MFA_RESCALE_TAU) {
-    const bool moved = __any((mx - rs.m) * c > tau);
+// Returns true when the reference moved (wave-uniform); m_old keeps the
+// previous running max, for the rescale factor move_alpha(m_old, m, c) the
+// caller applies to O and l only then.  tau_c = tau / c.
+__device__ __forceinline__ bool qb_move(RowState& rs, float mx, float c, float tau_c, float& m_old) {
     m_old = rs.m;
-    rs.m = moved ? fmax_nn(rs.m, mx) : rs.m;
-    mu = (rs.m == -INFINITY) ? 0.f : rs.m * c;
+    const bool moved = __any(mx > rs.thr);
+    if (moved) {
+        rs.m = fmax_nn(rs.m, mx);
+        rs.mu = rs.m == -INFINITY ? 0.f : rs.m * c;
+        rs.thr = rs.m + tau_c;
+    }
     return moved;
 }
 __device__ __forceinline__ float move_alpha(float m_old, float m_new, float c) {
     return m_new == -INFINITY ? 1.f : fast_exp2((m_old - m_new) * c);
+}
+// qb_move with the rescale of l; alpha is the factor for O when it returns true
+__device__ __forceinline__ bool qb_update(RowState& rs, float mx, float c, float tau_c, float& alpha) {
+    float m_old;
+    alpha = 1.f;
+    const bool moved = qb_move(rs, mx, c, tau_c, m_old);
+    if (moved) {
+        alpha = move_alpha(m_old, rs.m, c);
+        rs.l *= alpha;
+    }
+    return moved;
 }
 
 template <int DB>
@@ -291,6 +292,52 @@ __device__ __forceinline__ void qb_probs16(const f32x16_t (&s)[NKB], u32x4_t (&p
     l += acc[0] + acc[1];
 }
 
+// qb_probs16 in two passes: the rounded probabilities, then (called later)
+// their row sum.  The same values are summed in the same order, so l is
+// bit-identical to qb_probs16's.
+template <int NKB, bool IS_BF16>
+__device__ __forceinline__ void qb_probs16_only(const f32x16_t (&s)[NKB], u32x4_t (&pw)[NKB][2], float mu,
+                                                float c) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float p0 = fast_exp2(fmaf(s[kb][8 * st + 2 * w], c, -mu));
+                const float p1 = fast_exp2(fmaf(s[kb][8 * st + 2 * w + 1], c, -mu));
+                if constexpr (IS_BF16) {
+                    const bf16x2_t pk = {(__bf16)p0, (__bf16)p1};
+                    pw[kb][st][w] = __builtin_bit_cast(uint32_t, pk);
+                } else {
+                    const f16x2_t pk = {(_Float16)p0, (_Float16)p1};
+                    pw[kb][st][w] = __builtin_bit_cast(uint32_t, pk);
+                }
+            }
+}
+template <int NKB, bool IS_BF16>
+__device__ __forceinline__ float qb_sum16(const u32x4_t (&pw)[NKB][2]) {
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                // (a plain copy first: a bit cast straight from a vector element
+                // reads element 0 with this compiler)
+                const uint32_t x = pw[kb][st][w];
+                if constexpr (IS_BF16) {
+                    const bf16x2_t one = {(__bf16)1.f, (__bf16)1.f};
+                    acc[w & 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), one, acc[w & 1], false);
+                } else {
+                    const f16x2_t one = {(_Float16)1.f, (_Float16)1.f};
+                    acc[w & 1] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), one, acc[w & 1], false);
+                }
+            }
+    return acc[0] + acc[1];
+}
+
 template <int NKB>
 __device__ __forceinline__ void qb_probs32(f32x16_t (&s)[NKB], float& l, float mu, float c) {
     float acc[2] = {0.f, 0.f};
@@ -324,7 +371,7 @@ __device__ __forceinline__ void store_out_l(const KArgs& a, const SeqView& sv, f
         const int qrow = qrow0 + 32 * qb + l32;
         if (qrow >= sv.Lq) continue;
         if (sv.lse && half == 0) {
-            const float mu = rs[qb].m == -INFINITY ? 0.f : rs[qb].m * c;
+            const float mu = rs[qb].mu;
             sv.lse[qrow] = l > 0.f ? (mu + __builtin_amdgcn_logf(l)) * kLn2 : -INFINITY;
         }
 #pragma unroll
@@ -376,7 +423,7 @@ __device__ __forceinline__ void store_partial(const KArgs& a, int Lq, int unit, 
         if (qrow >= Lq) continue;
         const int64_t row = ((int64_t)split * a.U + unit) * a.Lq + qrow;
         if (half == 0) {
-            const float mu = rs[qb].m == -INFINITY ? 0.f : rs[qb].m * c;
+            const float mu = rs[qb].mu;
             a.ws_lse[row] = l > 0.f ? mu + __builtin_amdgcn_logf(l) : -INFINITY;
         }
         float* dst = a.ws_o + row * a.ws_ld;
@@ -516,8 +563,7 @@ mfa_fwd16_kernel(KArgs a) {
         rs[qb].lo = key_lo(a, rs[qb].center);
         rs[qb].hi = key_hi(a, rs[qb].center, Lk);
         rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
-        rs[qb].m = -INFINITY;
-        rs[qb].l = 0.f;
+        row_reset(rs[qb]);
     }
     f32x16_t o[QB][DB];
 #pragma unroll
@@ -531,6 +577,7 @@ mfa_fwd16_kernel(KArgs a) {
     // grouped-query decode rows: their results do not depend on which rows
     // share a wave, so packed heads equal unpacked ones bit for bit
     const float tau = (Lq == 1 || a.decode_pack) ? 0.f : (float)MFA_RESCALE_TAU;
+    const float tau_c = tau / c;
 
     // ---- key range of the workgroup and of this wavefront
     const int qlast = min(q0 + BM, Lq) - 1;
@@ -659,9 +706,9 @@ mfa_fwd16_kernel(KArgs a) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
             qb_transform<NKB, BIAS, MASKED>(a, sacc[qb], rs[qb], j, half);
-            float mu, alpha;
-            if (qb_update(rs[qb], qb_max<NKB>(sacc[qb]), c, mu, alpha, tau)) scale_rows<DB>(o[qb], alpha);
-            qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, mu, c);
+            float alpha;
+            if (qb_update(rs[qb], qb_max<NKB>(sacc[qb]), c, tau_c, alpha)) scale_rows<DB>(o[qb], alpha);
+            qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, rs[qb].mu, c);
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db)
@@ -735,7 +782,7 @@ mfa_fwd16_kernel(KArgs a) {
         for (int qb = 0; qb < QB; ++qb) {
             const int nm = (qb + 1 < QB ? kQK : 0) + (qb > 0 ? kPV : 0);
             qb_transform<NKB, BIAS, false>(a, sacc[qb], rs[qb], j, half);
-            float mpart[2] = {-INFINITY, -INFINITY}, alpha = 1.f, mu = 0.f;
+            float mpart[2] = {-INFINITY, -INFINITY}, alpha = 1.f;
             float lacc[2] = {0.f, 0.f};
             bool moved = false;
 #pragma unroll
@@ -749,7 +796,7 @@ mfa_fwd16_kernel(KArgs a) {
                         mpart[1] = fmax_nn(mpart[1], sacc[qb][ci][r + 1]);
                     }
                 } else if (ci == NKB) {  // merge halves, new running max
-                    moved = qb_update(rs[qb], max_halves(fmax_nn(mpart[0], mpart[1])), c, mu, alpha, tau);
+                    moved = qb_update(rs[qb], max_halves(fmax_nn(mpart[0], mpart[1])), c, tau_c, alpha);
                 } else if (ci < NKB + 1 + DB) {  // rescale O rows (only if some row's max moved)
                     const int db = ci - NKB - 1;
                     if (moved) {
@@ -760,8 +807,8 @@ mfa_fwd16_kernel(KArgs a) {
                     const int g = ci - NKB - 1 - DB, kb = g / 2, st = g % 2;
 #pragma unroll
                     for (int w = 0; w < 4; ++w) {
-                        const float p0 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w], c, -mu));
-                        const float p1 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w + 1], c, -mu));
+                        const float p0 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w], c, -rs[qb].mu));
+                        const float p1 = fast_exp2(fmaf(sacc[qb][kb][8 * st + 2 * w + 1], c, -rs[qb].mu));
                         pw[qb][kb][st][w] = pack_and_sum<IS_BF16>(p0, p1, lacc[w & 1]);
                     }
                     // (the block's sum joins l at the end, as in qb_probs16)
@@ -946,8 +993,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
         rs[qb].lo = key_lo(a, rs[qb].center);
         rs[qb].hi = key_hi(a, rs[qb].center, Lk);
         rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
-        rs[qb].m = -INFINITY;
-        rs[qb].l = 0.f;
+        row_reset(rs[qb]);
         const int r0 = wq0 + 32 * qb;
         const int r1 = max(min(r0 + 31, Lq - 1), r0);
         lo_max[qb] = key_lo(a, r1 + dq);
@@ -964,6 +1010,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
     // per-row rescales for single-row sequences, as in the 4-wavefront kernel
     // (the two kernels then agree bit for bit on every shape)
     const float tau = Lq == 1 ? 0.f : (float)MFA_RESCALE_TAU;
+    const float tau_c = tau / c;
 
     // ---- key range of the workgroup
     const int qlast = min(q0 + BM, Lq) - 1;
@@ -1173,16 +1220,24 @@ mfa_fwd16_pp_kernel(KArgs a) {
         // both query blocks' max, update and probabilities in one branch-free
         // stretch (independent chains for the scheduler to interleave); the
         // rare rescale of O follows (O is next read by PV in the next phase)
-        float mx[QB], mu[QB], m_old[QB], bsum[QB];
+        float mx[QB], m_old[QB], bsum[QB];
         bool moved[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) mx[qb] = qb_max<NKB>(sacc[qb]);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_move(rs[qb], mx[qb], c, mu[qb], m_old[qb], tau);
+        for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_move(rs[qb], mx[qb], c, tau_c, m_old[qb]);
+        if constexpr (MFA_PP_LATE_SUM && DP <= 64) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            bsum[qb] = 0.f;
-            qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], bsum[qb], mu[qb], c);
+            for (int qb = 0; qb < QB; ++qb) qb_probs16_only<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].mu, c);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) bsum[qb] = qb_sum16<NKB, IS_BF16>(pw[qb]);
+        } else {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                bsum[qb] = 0.f;
+                qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], bsum[qb], rs[qb].mu, c);
+            }
         }
         // the rare rescale of O and l: alpha only when the reference moved
 #pragma unroll
@@ -1329,14 +1384,14 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
     rs[0].lo = key_lo(a, rs[0].center);
     rs[0].hi = key_hi(a, rs[0].center, Lk);
     rs[0].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
-    rs[0].m = -INFINITY;
-    rs[0].l = 0.f;
+    row_reset(rs[0]);
     f32x16_t o[QB][DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[0][db][r] = 0.f;
     const float c = BIAS ? kLog2e : a.scale_log2;
+    const float tau_c = (float)MFA_RESCALE_TAU / c;
 
     const int qlast = min(q0 + BM, Lq) - 1;
     const int klo = key_lo(a, q0 + dq);
@@ -1397,9 +1452,9 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
             }
         }
         qb_transform<NKB, BIAS, MASKED>(a, sacc, rs[0], j, half);
-        float mu, alpha;
-        if (qb_update(rs[0], qb_max<NKB>(sacc), c, mu, alpha)) scale_rows<DB>(o[0], alpha);
-        qb_probs32<NKB>(sacc, rs[0].l, mu, c);
+        float alpha;
+        if (qb_update(rs[0], qb_max<NKB>(sacc), c, tau_c, alpha)) scale_rows<DB>(o[0], alpha);
+        qb_probs32<NKB>(sacc, rs[0].l, rs[0].mu, c);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
