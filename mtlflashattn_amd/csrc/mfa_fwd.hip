@@ -94,14 +94,27 @@ constexpr int kWaves = 4;
 #ifndef MFA_PP_PRIO
 #define MFA_PP_PRIO 1
 #endif
+// ping-pong kernel with four wavefronts per SIMD (512-row tiles of one 32-row
+// query block per wavefront) at head dims up to 64, and its operand read-ahead
+#ifndef MFA_PP_NW16
+#define MFA_PP_NW16 0
+#endif
+#ifndef MFA_PP_AHEAD16
+#define MFA_PP_AHEAD16 1
+#endif
 // ping-pong kernel: group 1 issues its K/V loads in its MFMA phase
 #ifndef MFA_PP_DMA_A
 #define MFA_PP_DMA_A 1
 #endif
 // ping-pong kernel at head dims up to 64: the row sums of a block's rounded
-// probabilities are issued after all of its probabilities, late in the
-// softmax phase, when the partner wavefront's MFMAs are mostly done (dot2
-// instructions wait while the other wavefront of the SIMD issues MFMAs)
+// probabilities are issued at the start of the next MFMA phase (the softmax
+// phase is the longer one there, and dot2 instructions wait while the other
+// wavefront of the SIMD issues MFMAs, which it does not at that point) ...
+#ifndef MFA_PP_SUM_IN_A
+#define MFA_PP_SUM_IN_A 1
+#endif
+// ... or, with that off, after all of the block's probabilities, late in the
+// softmax phase, when the partner wavefront's MFMAs are mostly done
 #ifndef MFA_PP_LATE_SUM
 #define MFA_PP_LATE_SUM 1
 #endif
@@ -925,10 +938,11 @@ mfa_fwd16_kernel(KArgs a) {
 // chunks of each row XOR-swizzled, so the K operand reads (one row per lane)
 // and the transposed V reads (four rows per 16 lanes) are free of bank
 // conflicts.
-template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4)))
 mfa_fwd16_pp_kernel(KArgs a) {
-    constexpr int NW = 8;              // wavefronts
+    static_assert(NW == 8 || NW == 16, "two or four wavefronts per SIMD");
+    constexpr bool SUM_IN_A = MFA_PP_SUM_IN_A && DP <= 64;
     constexpr int NT = NW * 64;        // threads
     constexpr int BM = NW * QB * 32;   // query rows per workgroup
     constexpr int BN = NKB * 32;       // keys per K/V block
@@ -1138,7 +1152,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
         constexpr int NPV = DB * NKB * 2;
         constexpr int NQK = NKB * DS;
         constexpr int NS = NPV + NQK;
-        constexpr int AH = QB == 1 ? MFA_PP_AHEAD1 : MFA_PP_AHEAD;
+        constexpr int AH = NW == 16 ? MFA_PP_AHEAD16 : QB == 1 ? MFA_PP_AHEAD1 : MFA_PP_AHEAD;
         const uint16_t* vt = vst0 + ((u + NST - 1) % NST) * TILE;
         const uint16_t* kt = kst0 + (u % NST) * TILE;
         const uint16_t* kp[DS];
@@ -1192,6 +1206,20 @@ mfa_fwd16_pp_kernel(KArgs a) {
         };
         if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(MFA_PP_PRIO);
         static_for<AH>(load_step);
+        if constexpr (SUM_IN_A) {
+            // row sums of P(u-1), whose rescale (if any) B(u-1) applied to l
+            // (the pins keep the compiler from moving the sums into B)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int st = 0; st < 2; ++st) pin(pw[qb][kb][st]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) rs[qb].l += qb_sum16<NKB, IS_BF16>(pw[qb]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) pin(rs[qb].l);
+        }
         __builtin_amdgcn_sched_barrier(0);
         static_for<NS>([&](auto ic) __attribute__((always_inline)) {
             constexpr int i = decltype(ic)::value;
@@ -1226,7 +1254,13 @@ mfa_fwd16_pp_kernel(KArgs a) {
         for (int qb = 0; qb < QB; ++qb) mx[qb] = qb_max<NKB>(sacc[qb]);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) moved[qb] = qb_move(rs[qb], mx[qb], c, tau_c, m_old[qb]);
-        if constexpr (MFA_PP_LATE_SUM && DP <= 64) {
+        if constexpr (SUM_IN_A) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                qb_probs16_only<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].mu, c);
+                bsum[qb] = 0.f;  // (added in the next MFMA phase)
+            }
+        } else if constexpr (MFA_PP_LATE_SUM && DP <= 64) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) qb_probs16_only<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].mu, c);
             __builtin_amdgcn_sched_barrier(0);
@@ -1247,8 +1281,10 @@ mfa_fwd16_pp_kernel(KArgs a) {
                 scale_rows<DB>(o[qb], alpha);
                 rs[qb].l *= alpha;
             }
+        if constexpr (!SUM_IN_A) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) rs[qb].l += bsum[qb];
+            for (int qb = 0; qb < QB; ++qb) rs[qb].l += bsum[qb];
+        }
         // (the row sums stay in this phase too)
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) pin(rs[qb].l);
@@ -1526,12 +1562,12 @@ KernelCfg cfg16(const char* name, bool paged) {
                            : (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, false>,
                      BM, BN, 2 * (kv > qs ? kv : qs), name};
 }
-template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, int NW = 8>
 KernelCfg cfg16pp(const char* name) {
-    constexpr int BM = 8 * QB * 32, BN = NKB * 32;
+    constexpr int BM = NW * QB * 32, BN = NKB * 32;
     constexpr int kv = 2 * 3 * BN * DP, qs = BM * (DP + 8);  // three K and three V stages / Q staging
-    return KernelCfg{mfa_fwd16_pp_kernel<DP, QB, NKB, IS_BF16, BIAS>, BM, BN, 2 * (kv > qs ? kv : qs) + 16, name,
-                     512};
+    return KernelCfg{mfa_fwd16_pp_kernel<DP, QB, NKB, IS_BF16, BIAS, NW>, BM, BN, 2 * (kv > qs ? kv : qs) + 16, name,
+                     NW * 64};
 }
 template <int DP, int NKB, bool BIAS>
 KernelCfg cfg32(const char* name, bool paged) {
@@ -1577,6 +1613,13 @@ KernelCfg select16(int dp, bool fills_chip, bool paged, bool pp256) {
         if (dp == 32)
             return cfg16pp<32, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,1,2>" : "mfa_fwd16pp<f16,d32,1,2>");
         return cfg16pp<64, 1, 2, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,1,2>" : "mfa_fwd16pp<f16,d64,1,2>");
+    }
+    if constexpr (MFA_PP_NW16 && !BIAS) {  // four wavefronts per SIMD (with a bias they spill)
+        if (MFA_PINGPONG && fills_chip && dp <= 64) {
+            if (dp == 32)
+                return cfg16pp<32, 1, 2, IS_BF16, BIAS, 16>(IS_BF16 ? "mfa_fwd16pp<bf16,d32,1,2,16w>" : "mfa_fwd16pp<f16,d32,1,2,16w>");
+            return cfg16pp<64, 1, 2, IS_BF16, BIAS, 16>(IS_BF16 ? "mfa_fwd16pp<bf16,d64,1,2,16w>" : "mfa_fwd16pp<f16,d64,1,2,16w>");
+        }
     }
     if (MFA_PINGPONG && fills_chip && dp <= 64) {
         if (dp == 32)
