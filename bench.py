@@ -17,8 +17,9 @@ Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
 Before the W warm-up steps the step also runs untimed for --clock-warmup
 seconds (default 1.0, declared in the line as clock_warmup_s/_steps) so that
 the K timed steps see the steady-state shader clock.
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7|8]
-(6-8: HBM-bound short-L shapes, roofline in GB/s against 8 TB/s; 8 runs split-KV)
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7|8|9|10]
+(6-10: HBM-bound short-L, decode and tiny-key shapes, roofline in GB/s against
+8 TB/s; 8 runs split-KV)
 """
 from __future__ import annotations
 
@@ -133,6 +134,20 @@ def make_config(cfg: int):
                     algo=4 * pairs * D, varlen=None, hbm_bytes=2 * (2 * B * Hq * D + 2 * B * Lk * Hkv * D),
                     workload=f"cfg9 (HBM-bound, not a BASELINE config): bf16 B={B} Lq=1 Lk={Lk} Hq={Hq} Hkv={Hkv} "
                              f"D={D} causal (grouped-query decode), seed 9")
+    if cfg == 10:
+        # not a BASELINE config: tiny-key cross-attention (image conditioning),
+        # the shape of the reference's trace example (README.md:141-145:
+        # bf16 D=128 Lq=26136 Lk=5); Q and O dominate the bytes (HBM-bound)
+        g = torch.Generator().manual_seed(10)
+        B, Lq, Lk, H, D = 1, 26136, 5, 16, 128
+        q = torch.randn(B, Lq, H, D, generator=g).to(dev, torch.bfloat16)
+        k = torch.randn(B, Lk, H, D, generator=g).to(dev, torch.bfloat16)
+        v = torch.randn(B, Lk, H, D, generator=g).to(dev, torch.bfloat16)
+        pairs = B * H * Lq * Lk
+        return dict(q=q, k=k, v=v, kw=dict(causal=False), dtype="bf16", D=D, formula=4 * pairs * D,
+                    algo=4 * pairs * D, varlen=None, hbm_bytes=2 * (2 * B * Lq * H * D + 2 * B * Lk * H * D),
+                    workload=f"cfg10 (HBM-bound, not a BASELINE config): bf16 B={B} Lq={Lq} Lk={Lk} H={H} D={D} "
+                             f"non-causal (tiny-key cross-attention), seed 10")
     raise SystemExit(f"unknown config {cfg}")
 
 
@@ -196,9 +211,9 @@ def cpu_baseline(cfg: int, budget_s: float = 12.0):
         kws = {kk: vv for kk, vv in kw.items() if kk != "alibi_slopes"}
         al = kw["alibi_slopes"][:heads] if "alibi_slopes" in kw else None
         fn = lambda: chunked.flash_attn_func(qs, ks, vs, alibi_slopes=al, rows=rows, **kws)  # noqa: E731
-        L = q.shape[1]
-        nrows = 2048 if rows else L
-        flops = 4 * heads * nrows * L * c["D"] // (2 if (c["kw"].get("causal") and not rows) else 1)
+        Lq, Lk = q.shape[1], k.shape[1]
+        nrows = 2048 if rows else Lq
+        flops = 4 * heads * nrows * Lk * c["D"] // (2 if (c["kw"].get("causal") and not rows) else 1)
         sample = f"{heads} of {H} heads" + (", last 2048 query rows" if rows else ", all rows") + \
             f" (full Lq x Lk grid computed, as the reference torch path does)"
     fn()  # warm-up
@@ -249,7 +264,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8, 9],
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8, 9, 10],
                     help="BASELINE config 2-5 (default 2, the headline); 6-9 are HBM-bound short-L / decode "
                          "shapes (roofline in GB/s; 8 runs split-KV, 9 is grouped-query decode)")
     ap.add_argument("--clock-warmup", type=float, default=1.0,

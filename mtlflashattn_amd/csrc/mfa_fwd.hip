@@ -1362,6 +1362,217 @@ mfa_fwd16_pp_kernel(KArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// 16-bit kernel for at most 32 keys per sequence (cross-attention to a short
+// conditioning sequence: many query rows, a handful of keys).  The keys fit
+// one 32-key block, so each wavefront keeps K and V^T as MFMA operands in
+// registers (staged once through LDS, in the 4-wavefront kernel's layout)
+// and streams NQ 32-row query blocks through them: Q fragments straight from
+// global memory, S^T = K Q^T, the online softmax of a single block, O^T = V^T
+// P^T, O stored.  No barrier after the set-up: the kernel moves Q in and O out
+// (HBM-bound).  Per row it performs the 4-wavefront kernel's operations in
+// its order (its second 32-key block and its second PV step add only zeros
+// there), so both give the same bits.
+#ifndef MFA_TK_BLOCKS
+#define MFA_TK_BLOCKS 1
+#endif
+#ifndef MFA_TK
+#define MFA_TK 1
+#endif
+// wavefronts per SIMD the tiny-key kernel is register-budgeted for
+#ifndef MFA_TK_WAVES
+#define MFA_TK_WAVES 3
+#endif
+// query rows from which the tiny-key kernel is chosen
+#ifndef MFA_TK_MIN_ROWS
+#define MFA_TK_MIN_ROWS 128
+#endif
+template <int DP, bool IS_BF16, bool BIAS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MFA_TK_WAVES)))
+mfa_fwd16_tk_kernel(KArgs a) {
+    constexpr int DS = DP / 16, DB = DP / 32;
+    constexpr int NQ = MFA_TK_BLOCKS;          // 32-row query blocks per wavefront
+    constexpr int BM = kWaves * NQ * 32;       // query rows per workgroup
+    // LDS row stride (elements) of K, V and the Q / O blocks: +16 bytes
+    // against bank conflicts in the row-per-lane reads (V is read once per
+    // workgroup, so its transposed reads need no wider padding)
+    constexpr int KST = DP + 8;
+    constexpr int VST = KST;
+    constexpr int CPR = DP / 8;                // 16-byte chunks per row
+    typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
+    // K, V (at most 32 rows each) and one 32-row Q / O block per wavefront
+    __shared__ __attribute__((aligned(16))) uint16_t kv_s[32 * KST + 32 * VST + kWaves * 32 * KST];
+    uint16_t* const tk_s = kv_s + 32 * KST + 32 * VST;
+
+    int b, hq, tile;
+    if (!decode_tile(a, blockIdx.x, b, hq, tile)) return;
+    const SeqView sv = seq_view<2>(a, b, hq);
+    const int q0 = tile * BM;
+    if (q0 >= sv.Lq) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, half = lane >> 5;
+    const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
+    const int dq = Lk - Lq;
+
+    // Q in and O out go through this wavefront's LDS block (32 rows), so that
+    // global reads and writes are row-contiguous: 16 lanes cover a 256-byte
+    // row (MFMA operand order would touch 32 rows in 16-32 byte pieces).  The
+    // next block's rows are loaded into registers before this block's MFMAs,
+    // the first block's during the K/V set-up.
+    constexpr int QCH = 32 * CPR / 64;  // 16-byte chunks per lane and block
+    uint16_t* const qo = tk_s + wave * (32 * KST);
+    u32x4_t qn[QCH];
+    // (buffer loads through a resource sized to the block's valid rows:
+    // rows past the sequence and chunks past the head dim read zero, with no
+    // branches, so the waits on them are counted exactly)
+    auto load_q = [&](int n) __attribute__((always_inline)) {
+        const int r0 = q0 + (wave * NQ + n) * 32;
+        const int rows = min(Lq - r0, 32);
+        const int bytes = __builtin_amdgcn_readfirstlane(rows > 0 ? (int)(((int64_t)(rows - 1) * a.qs + D) * 2) : 0);
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(sv.q + (int64_t)max(r0, 0) * a.qs * 2), (short)0, bytes, kBufferDword3);
+#pragma unroll
+        for (int i = 0; i < QCH; ++i) {
+            const int ch = lane + 64 * i, col = (ch % CPR) * 8;
+            const uint32_t off = col < D ? (uint32_t)(((int64_t)(ch / CPR) * a.qs + col) * 2) : 0x80000000u;
+            qn[i] = __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0);
+        }
+    };
+
+    // ---- K and V rows (zero past the sequence and the head dim) -> LDS
+    uint16_t* const vs = kv_s + 32 * KST;
+    constexpr int KVC = (32 * CPR + kThreads - 1) / kThreads;  // chunks per thread
+    u32x4_t kk[KVC], vv[KVC];
+    {
+        const int kbytes = __builtin_amdgcn_readfirstlane(Lk > 0 ? (int)(((int64_t)(Lk - 1) * a.ks + D) * 2) : 0);
+        const int vbytes = __builtin_amdgcn_readfirstlane(Lk > 0 ? (int)(((int64_t)(Lk - 1) * a.vs + D) * 2) : 0);
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)sv.k, (short)0, kbytes, kBufferDword3);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)sv.v, (short)0, vbytes, kBufferDword3);
+#pragma unroll
+        for (int i = 0; i < KVC; ++i) {
+            const int ch = tid + kThreads * i, row = ch / CPR, col = (ch % CPR) * 8;
+            const bool in = ch < 32 * CPR && col < D;
+            kk[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                kr, in ? (uint32_t)(((int64_t)row * a.ks + col) * 2) : 0x80000000u, 0, 0);
+            vv[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                vr, in ? (uint32_t)(((int64_t)row * a.vs + col) * 2) : 0x80000000u, 0, 0);
+        }
+    }
+    load_q(0);  // (after the K/V loads: their results are waited for first)
+#pragma unroll
+    for (int i = 0; i < KVC; ++i) {
+        const int ch = tid + kThreads * i, row = ch / CPR, col = (ch % CPR) * 8;
+        if (KVC * kThreads == 32 * CPR || ch < 32 * CPR) {
+            *reinterpret_cast<u32x4_t*>(kv_s + row * KST + col) = kk[i];
+            *reinterpret_cast<u32x4_t*>(vs + row * VST + col) = vv[i];
+        }
+    }
+    __syncthreads();
+    // K operand: row l32, k-slots 16*s + 8*half.. ; V^T operand of PV step
+    // st: the 4-wavefront kernel's transposed reads (lane i of a 16-lane group
+    // addresses 4 elements of key row i/4, lane j receives element j of rows 0..3)
+    op_t kf[DS], vf[DB][2];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) kf[s] = *reinterpret_cast<const op_t*>(kv_s + l32 * KST + 16 * s + 8 * half);
+    const int tr_row = 4 * half + ((lane & 15) >> 2);
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const uint16_t* p0 = vs + (16 * st + tr_row) * VST + 32 * db + tr_col;
+            const uint16_t* p1 = p0 + 8 * VST;
+            typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+            typedef __attribute__((address_space(3))) fp16x4_t* lp;
+            const u32x2_t lo = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p0)));
+            const u32x2_t hi = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lp)(p1)));
+            vf[db][st] = __builtin_bit_cast(op_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+        }
+    auto mfma16 = [](const op_t& x, const op_t& y, const f32x16_t& acc) {
+        if constexpr (IS_BF16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, acc, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, acc, 0, 0, 0);
+    };
+    const float c = BIAS ? kLog2e : a.scale_log2;
+    const float tau = (Lq == 1 || a.decode_pack) ? 0.f : (float)MFA_RESCALE_TAU;
+    const float tau_c = tau / c;
+    const float slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+    // a key past the second 16 never carries weight when Lk <= 16: one PV step
+    const bool two_steps = Lk > 16;
+
+#pragma unroll
+    for (int n = 0; n < NQ; ++n) {
+        const int wq0 = q0 + (wave * NQ + n) * 32;  // this wavefront's n-th block
+        if (wq0 >= Lq) break;
+        // rows -> LDS -> B operands (row l32, k-slots 16*s + 8*half..); the
+        // wave's own LDS operations complete in order
+#pragma unroll
+        for (int i = 0; i < QCH; ++i) {
+            const int ch = lane + 64 * i;
+            *reinterpret_cast<u32x4_t*>(qo + (ch / CPR) * KST + (ch % CPR) * 8) = qn[i];
+        }
+        op_t qf[DS];
+#pragma unroll
+        for (int s = 0; s < DS; ++s) qf[s] = *reinterpret_cast<const op_t*>(qo + l32 * KST + 16 * s + 8 * half);
+        if (n + 1 < NQ) load_q(n + 1);
+        const int row = wq0 + l32;
+        RowState rs[1];
+        rs[0].center = row + dq;
+        rs[0].lo = key_lo(a, rs[0].center);
+        rs[0].hi = key_hi(a, rs[0].center, Lk);
+        rs[0].slope = slope;
+        row_reset(rs[0]);
+        f32x16_t sacc[1];
+#pragma unroll
+        for (int s = 0; s < DS; ++s) sacc[0] = mfma16(kf[s], qf[s], s == 0 ? f32x16_t{} : sacc[0]);
+        qb_transform<1, BIAS, true>(a, sacc, rs[0], 0, half);
+        float alpha;
+        (void)qb_update(rs[0], qb_max<1>(sacc), c, tau_c, alpha);  // from the empty state: O is still zero
+        u32x4_t pw[1][2];
+        qb_probs16<1, IS_BF16>(sacc, pw, rs[0].l, rs[0].mu, c);
+        f32x16_t o[1][DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            o[0][db] = mfma16(vf[db][0], __builtin_bit_cast(op_t, pw[0][0]), f32x16_t{});
+            if (two_steps) o[0][db] = mfma16(vf[db][1], __builtin_bit_cast(op_t, pw[0][1]), o[0][db]);
+        }
+        if (a.out_f32) {  // the fp32 parity output: the common store
+            store_out<1, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
+            continue;
+        }
+        // normalised 16-bit rows -> LDS (this lane: row l32, d = 32*db + 8*g +
+        // 4*half..+3) -> row-contiguous global stores; the lse as elsewhere
+        const float l = sum_halves(rs[0].l);
+        const float inv = l > 0.f ? 1.f / l : 0.f;  // fully masked rows -> 0 (_kernel.py:85)
+        if (sv.lse && half == 0 && row < Lq)
+            sv.lse[row] = l > 0.f ? (rs[0].mu + __builtin_amdgcn_logf(l)) * kLn2 : -INFINITY;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float v0 = o[0][db][4 * g] * inv, v1 = o[0][db][4 * g + 1] * inv;
+                const float v2 = o[0][db][4 * g + 2] * inv, v3 = o[0][db][4 * g + 3] * inv;
+                u32x2_t w;
+                if constexpr (IS_BF16) {
+                    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+                    w = __builtin_bit_cast(u32x2_t, bf16x4_t{(__bf16)v0, (__bf16)v1, (__bf16)v2, (__bf16)v3});
+                } else {
+                    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
+                    w = __builtin_bit_cast(u32x2_t, f16x4_t{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3});
+                }
+                *reinterpret_cast<u32x2_t*>(qo + l32 * KST + 32 * db + 8 * g + 4 * half) = w;
+            }
+#pragma unroll
+        for (int i = 0; i < QCH; ++i) {
+            const int ch = lane + 64 * i, orow = wq0 + ch / CPR, col = (ch % CPR) * 8;
+            const u32x4_t w = *reinterpret_cast<const u32x4_t*>(qo + (ch / CPR) * KST + col);
+            if (orow < Lq && col < D)
+                *reinterpret_cast<u32x4_t*>(sv.o + ((int64_t)orow * a.os + col) * 2) = w;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // fp32 kernel: same structure with v_mfma_f32_32x32x2_f32.  K-slot layout of
 // the 32x32x2 MFMA: lane (half, x) supplies k = half, so QK^T step s uses
 // d = s + half*DP/2 and PV step r uses the key held in accumulator register r.
@@ -1568,6 +1779,20 @@ KernelCfg cfg16pp(const char* name) {
     constexpr int kv = 2 * 3 * BN * DP, qs = BM * (DP + 8);  // three K and three V stages / Q staging
     return KernelCfg{mfa_fwd16_pp_kernel<DP, QB, NKB, IS_BF16, BIAS, NW>, BM, BN, 2 * (kv > qs ? kv : qs) + 16, name,
                      NW * 64};
+}
+template <int DP, bool IS_BF16, bool BIAS>
+KernelCfg cfg16tk(const char* name) {
+    constexpr int BM = kWaves * MFA_TK_BLOCKS * 32;
+    return KernelCfg{mfa_fwd16_tk_kernel<DP, IS_BF16, BIAS>, BM, 32, 2 * 32 * (kWaves + 2) * (DP + 8), name};
+}
+template <bool IS_BF16, bool BIAS>
+KernelCfg select16tk(int dp) {
+    switch (dp) {
+        case 32: return cfg16tk<32, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16tk<bf16,d32>" : "mfa_fwd16tk<f16,d32>");
+        case 64: return cfg16tk<64, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16tk<bf16,d64>" : "mfa_fwd16tk<f16,d64>");
+        case 96: return cfg16tk<96, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16tk<bf16,d96>" : "mfa_fwd16tk<f16,d96>");
+        default: return cfg16tk<128, IS_BF16, BIAS>(IS_BF16 ? "mfa_fwd16tk<bf16,d128>" : "mfa_fwd16tk<f16,d128>");
+    }
 }
 template <int DP, int NKB, bool BIAS>
 KernelCfg cfg32(const char* name, bool paged) {
@@ -1932,8 +2157,18 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         else
             pp256 = prefer_pp256(p, geom.cus);
     }
+    // At most 32 keys per sequence under many query rows (cross-attention to
+    // a short conditioning sequence): the tiny-key kernel, which keeps the
+    // keys in registers and streams the query rows (measured at bf16 D=128
+    // Lq=26136 Lk=5 H=16: see the design notes)
+    const bool tiny_keys = MFA_TK && p->tile_hint == MFA_TILE_AUTO && din != MFA_DTYPE_F32 && !paged &&
+                           split_keys == 0 && p->seqlen_k <= 32 && p->seqlen_q >= MFA_TK_MIN_ROWS;
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp, paged) : select32<false>(dp, paged);
+    else if (tiny_keys && din == MFA_DTYPE_BF16)
+        plan->cfg = bias ? select16tk<true, true>(dp) : select16tk<true, false>(dp);
+    else if (tiny_keys)
+        plan->cfg = bias ? select16tk<false, true>(dp) : select16tk<false, false>(dp);
     else if (din == MFA_DTYPE_BF16)
         plan->cfg = bias ? select16<true, true>(dp, fills_chip, paged, pp256)
                          : select16<true, false>(dp, fills_chip, paged, pp256);
