@@ -420,6 +420,63 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
     store_out_l<QB, DB, IS_BF16>(a, sv, o, rs, lsum, qrow0, lane, c);
 }
 
+// store_out with the 16-bit rows routed through this wavefront's LDS block
+// `ls` (32*QB rows of ST elements), so that the global stores are
+// row-contiguous -- 16 lanes per 256-byte row -- instead of 32 rows in
+// 8-byte pieces per instruction.  The same values as store_out; the fp32
+// parity output keeps the direct store.
+#ifndef MFA_LDS_OSTORE
+#define MFA_LDS_OSTORE 1
+#endif
+template <int QB, int DB, bool IS_BF16, int ST>
+__device__ __forceinline__ void store_out_rows(const KArgs& a, const SeqView& sv, f32x16_t (&o)[QB][DB],
+                                               const RowState (&rs)[QB], int qrow0, int lane, float c,
+                                               uint16_t* ls) {
+    float lsum[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) lsum[qb] = sum_halves(rs[qb].l);
+    if (!MFA_LDS_OSTORE || a.out_f32) {
+        store_out_l<QB, DB, IS_BF16>(a, sv, o, rs, lsum, qrow0, lane, c);
+        return;
+    }
+    // (a fresh copy of the lane id: addresses derived from it are not shared
+    // with the main loop's, which would keep them live across the loop)
+    asm volatile("" : "+v"(lane));
+    const int l32 = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const float l = lsum[qb];
+        const float inv = l > 0.f ? 1.f / l : 0.f;  // fully masked rows -> 0 (_kernel.py:85)
+        const int qrow = qrow0 + 32 * qb + l32;
+        if (sv.lse && half == 0 && qrow < sv.Lq)
+            sv.lse[qrow] = l > 0.f ? (rs[qb].mu + __builtin_amdgcn_logf(l)) * kLn2 : -INFINITY;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float v0 = o[qb][db][4 * g] * inv, v1 = o[qb][db][4 * g + 1] * inv;
+                const float v2 = o[qb][db][4 * g + 2] * inv, v3 = o[qb][db][4 * g + 3] * inv;
+                u32x2_t w;
+                if constexpr (IS_BF16) {
+                    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+                    w = __builtin_bit_cast(u32x2_t, bf16x4_t{(__bf16)v0, (__bf16)v1, (__bf16)v2, (__bf16)v3});
+                } else {
+                    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
+                    w = __builtin_bit_cast(u32x2_t, f16x4_t{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3});
+                }
+                *reinterpret_cast<u32x2_t*>(ls + (32 * qb + l32) * ST + 32 * db + 8 * g + 4 * half) = w;
+            }
+    }
+    constexpr int CPR = DB * 4;                 // 16-byte chunks per row
+    constexpr int NCH = 32 * QB * CPR / 64;     // per lane
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int ch = lane + 64 * i, r = ch / CPR, col = (ch % CPR) * 8;
+        const u32x4_t w = *reinterpret_cast<const u32x4_t*>(ls + r * ST + col);
+        const int qrow = qrow0 + r;
+        if (qrow < sv.Lq && col < a.D) *reinterpret_cast<u32x4_t*>(sv.o + ((int64_t)qrow * a.os + col) * 2) = w;
+    }
+}
 
 // Split-KV partial of one chunk: O normalised by the chunk's own row sum and
 // the chunk's log2-sum-exp lse = mu + log2(l) (probabilities were
@@ -913,8 +970,9 @@ mfa_fwd16_kernel(KArgs a) {
 
     if (a.nsplit > 1)
         store_partial<QB, DB>(a, Lq, b * a.Hq + hq, split, o, rs, c, wq0, lane);
-    else
-        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
+    else  // (the loop's last barrier released the LDS)
+        store_out_rows<QB, DB, IS_BF16, KST>(a, sv, o, rs, wq0, lane, c,
+                                             smem + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * QB * 32 * KST);
 }
 
 // ----------------------------------------------------------------------------
@@ -1356,9 +1414,11 @@ mfa_fwd16_pp_kernel(KArgs a) {
         run(std::integral_constant<int, 0>{});
     else
         run(std::integral_constant<int, 1>{});
-    // no direct-to-LDS write may land after the workgroup's LDS is released
+    // no direct-to-LDS write may land after the workgroup's LDS is released,
+    // nor in the O blocks below (every wavefront's loads done, then a barrier)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
+    __syncthreads();
+    store_out_rows<QB, DB, IS_BF16, KST>(a, sv, o, rs, wq0, lane, c, smem + wave * QB * 32 * KST);
 }
 
 // ----------------------------------------------------------------------------
