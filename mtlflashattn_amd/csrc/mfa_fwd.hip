@@ -425,6 +425,9 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
 // row-contiguous -- 16 lanes per 256-byte row -- instead of 32 rows in
 // 8-byte pieces per instruction.  The same values as store_out; the fp32
 // parity output keeps the direct store.
+#ifndef MFA_ALIBI_REVERSE
+#define MFA_ALIBI_REVERSE 1
+#endif
 #ifndef MFA_LDS_OSTORE
 #define MFA_LDS_OSTORE 1
 #endif
@@ -664,6 +667,14 @@ mfa_fwd16_kernel(KArgs a) {
         jbeg = j0;
         kend = min(Lk, c1);
     }
+    // Key blocks run from the last to the first under ALiBi: scores fall with
+    // the distance to the diagonal, so the first block holds the row maxima
+    // and later blocks rarely move them (no O rescales).  Block it of the
+    // walk, it = 0 .. nblk-1; it = nblk, nblk+1 (the pipelined prefetch past
+    // the walk) fall outside [jbeg, jbeg + nblk*BN) and load nothing.
+    const bool rev = BIAS && DP > 64 && MFA_ALIBI_REVERSE && a.alibi != nullptr;
+    const int jfirst = rev ? jbeg + (nblk - 1) * BN : jbeg, jstep = rev ? -BN : BN;
+    auto blk = [&](int it) { return jfirst + it * jstep; };
     const int wlast = min(wq0 + QB * 32, Lq) - 1;  // < wq0 when the wave has no rows
     const bool wave_live = wlast >= wq0;
     const int w_lo_first = key_lo(a, wq0 + dq), w_lo_last = key_lo(a, wlast + dq);
@@ -687,16 +698,19 @@ mfa_fwd16_kernel(KArgs a) {
         lds_off[i] = (cc < BN * CPR) ? row * KST + col : -1;
         vlds_off[i] = (cc < BN * CPR) ? row * VST + col : -1;
     }
-    auto gload = [&](int j) {
+    auto gload = [&](int j0) {
         // rows <= 0 (a block past the sequence, loaded branch-free by the
-        // pipelined path) gives an empty resource: every lane reads zero
-        // (computed without branches, so the pipelined block stays one basic block)
+        // pipelined path) or a block before jbeg (past a reversed walk) gives
+        // an empty resource: every lane reads zero (computed without
+        // branches, so the pipelined block stays one basic block; the
+        // address is formed from a block inside the range)
+        const int j = max(j0, jbeg);
         const int rows = kend - j;
         const int rm1 = min(max(rows, 1), BN) - 1;
         bool kok, vok;
         const int64_t kbo = kv_block_off<PAGED>(a, sv, j, kend, a.kb, a.ks, kok);
         const int64_t vbo = kv_block_off<PAGED>(a, sv, j, kend, a.vb, a.vs, vok);
-        const int live = -(int)(rows > 0 && kok && vok);
+        const int live = -(int)(rows > 0 && j0 >= jbeg && kok && vok);
         // (readfirstlane: the sizes are uniform, but the clamp above selects
         // a vector med3, and a resource the backend sees in vector registers
         // gets a waterfall loop around every load)
@@ -900,7 +914,7 @@ mfa_fwd16_kernel(KArgs a) {
     };
 
     // the first K/V block's global loads run while Q is staged
-    if (nblk > 0) gload(jbeg);
+    if (nblk > 0) gload(blk(0));
 
     // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
     for (int c = tid; c < BM * CPR; c += kThreads) {
@@ -924,15 +938,15 @@ mfa_fwd16_kernel(KArgs a) {
     // (block 0's loads were issued before the Q tile was staged)
     if (nblk > 0) {
         swrite(0);
-        if (nblk > 1) gload(jbeg + BN);
+        if (nblk > 1) gload(blk(1));
         __syncthreads();
     }
     for (int it = 0; it < nblk; ++it) {
-        const int j = jbeg + it * BN;
+        const int j = blk(it);
         const int buf = it & 1;
         auto stage_next = [&]() {
             if (it + 1 < nblk) swrite(buf ^ 1);
-            if (it + 2 < nblk) gload(j + 2 * BN);
+            if (it + 2 < nblk) gload(blk(it + 2));
         };
         const bool skip = !wave_live || (j + BN - 1 < w_lo_first) || (j > w_hi_last);
         const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
@@ -947,7 +961,7 @@ mfa_fwd16_kernel(KArgs a) {
                     // through an empty resource (no memory access).
                     block_pipelined(kbuf, vtb, j, [&]() {
                         swrite(buf ^ 1);
-                        gload(j + 2 * BN);
+                        gload(blk(it + 2));
                     });
                 } else if constexpr (MFA_STAGE_IN_PV) {
                     block_pipelined(kbuf, vtb, j, stage_next);
@@ -1094,6 +1108,11 @@ mfa_fwd16_pp_kernel(KArgs a) {
         store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
         return;
     }
+    // key block of step u, last block first under ALiBi (as in the
+    // 4-wavefront kernel); steps past the walk load nothing
+    const bool rev = BIAS && DP > 64 && MFA_ALIBI_REVERSE && a.alibi != nullptr;
+    const int jfirst = rev ? jbeg + (nblk - 1) * BN : jbeg, jstep = rev ? -BN : BN;
+    auto blk = [&](int u) { return jfirst + u * jstep; };
 
     // ---- LDS tiles: chunk c of row r is stored in chunk slot c ^ swz(r).
     // The LDS serves 256 bytes per cycle: the 16 lanes of one ds_read_b128
@@ -1135,13 +1154,13 @@ mfa_fwd16_pp_kernel(KArgs a) {
     const int vfull = ((BN - 1) * (int)a.vs + D) * 2;
     auto load_block = [&](const char* base, int64_t bstride, int64_t stride, int full, uint16_t* dst, uint32_t off,
                           int u) __attribute__((always_inline)) {
-        const int j = jbeg + u * BN;
+        const int j0 = blk(u), j = max(j0, jbeg);
         const int rows = Lk - j;
         bool ok;
         const int64_t bo = kv_block_off<false>(a, sv, j, Lk, bstride, stride, ok);
         int bytes = full;
         if (rows < BN) bytes = rows > 0 ? ((rows - 1) * (int)stride + D) * 2 : 0;
-        if (!ok) bytes = 0;
+        if (!ok || j0 < jbeg) bytes = 0;
         lds_load16(reinterpret_cast<uint64_t>(base + bo * 2), (uint32_t)bytes, dst, off);
     };
     // loads of K block u into its stage u % NST (and likewise V); wave-uniform
@@ -1289,7 +1308,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
     };
     // B(u): online softmax of S(u) for both query blocks
     auto phase_b = [&](int u) __attribute__((always_inline)) {
-        const int j = jbeg + u * BN;
+        const int j = blk(u);
         // the softmax stays between the barriers: it starts from S as the
         // phase begins and its P is complete before the phase ends
 #pragma unroll
