@@ -147,10 +147,59 @@ struct RowState {
     float l;     // running row sum (this half-wave's keys)
 };
 
-template <int NKB, bool BIAS, bool MASKED>
+// tanh to within 2 ulp: the odd Taylor series of tanh through t^17 below
+// |y| = 0.6 (the next term is below 3e-8 of the result there), and
+// 1 - 2 / (exp(2|y|) + 1) above it, where the difference no longer cancels
+// (the exponential form loses the small values' relative precision: near
+// y = 0 it is off by up to 1.4e-7 absolute)
+__device__ __forceinline__ float precise_tanh(float y) {
+    const float t = fabsf(y);
+    float r;
+    if (t < 0.6f) {
+        const float u = t * t;
+        float p = 6404582.f / 10854718875.f;  // coefficients of t^17, t^15, ..., t^3
+        p = fmaf(p, u, -929569.f / 638512875.f);
+        p = fmaf(p, u, 21844.f / 6081075.f);
+        p = fmaf(p, u, -1382.f / 155925.f);
+        p = fmaf(p, u, 62.f / 2835.f);
+        p = fmaf(p, u, -17.f / 315.f);
+        p = fmaf(p, u, 2.f / 15.f);
+        p = fmaf(p, u, -1.f / 3.f);
+        r = fmaf(t * u, p, t);
+    } else {
+        r = 1.f - __fdiv_rn(2.f, fast_exp2(t * (2.f * kLog2e)) + 1.f);
+    }
+    return copysignf(r, y);
+}
+
+// Smallest ALiBi distance |center - j| over the row's valid keys [lo, hi].
+__device__ __forceinline__ int row_dmin(const RowState& rs) {
+    return max(0, max(rs.lo - rs.center, rs.center - rs.hi));
+}
+
+// PRECISE (the fp32 kernel): x = s*scale, softcap*tanh(x/softcap) with the
+// precise tanh, then ALiBi as -slope*(|d| - dmin), dmin = row_dmin (the
+// softmax is unchanged by a per-row constant; the lse store adds
+// -slope*dmin back).  A row hundreds of keys from every key then keeps its
+// scores near zero instead of near -slope*|d| (~ -10^2, where fp32 spacing
+// is ~1e-5).  The 16-bit kernels keep the fused forms.
+template <int NKB, bool BIAS, bool MASKED, bool PRECISE = false>
 __device__ __forceinline__ void qb_transform(const KArgs& a, f32x16_t (&s)[NKB], const RowState& rs, int j,
                                              int half) {
-    if constexpr (BIAS) {
+    if constexpr (BIAS && PRECISE) {
+        const float dmin = (float)row_dmin(rs);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            const float cf = (float)(rs.center - (j + 32 * kb + 4 * half));
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = s[kb][r] * a.scale;
+                if (a.softcap > 0.f) x = a.softcap * precise_tanh(__fdiv_rn(x, a.softcap));
+                if (a.alibi) x = fmaf(-rs.slope, fabsf(cf - (float)acc_row(r)) - dmin, x);
+                s[kb][r] = x;
+            }
+        }
+    } else if constexpr (BIAS) {
         // natural-log units: x = scale*s, soft-cap, ALiBi (_kernel.py:75-77)
         if (a.softcap > 0.f) {
             // c * tanh(x / c) = c - 2c / (exp(2x/c) + 1), the scale folded
@@ -1777,7 +1826,7 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
                 sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[s + 3], sacc[kb], 0, 0, 0);
             }
         }
-        qb_transform<NKB, BIAS, MASKED>(a, sacc, rs[0], j, half);
+        qb_transform<NKB, BIAS, MASKED, true>(a, sacc, rs[0], j, half);
         float alpha;
         if (qb_update(rs[0], qb_max<NKB>(sacc), c, tau_c, alpha)) scale_rows<DB>(o[0], alpha);
         qb_probs32<NKB>(sacc, rs[0].l, rs[0].mu, c);
@@ -1818,6 +1867,16 @@ __global__ void __launch_bounds__(kThreads) mfa_fwd32_kernel(KArgs a) {
 
     // fp32 output (out_f32 is implied for fp32 input)
     store_out<QB, DB, true>(a, sv, o, rs, wq0, lane, c);
+    if constexpr (BIAS) {
+        // the lse of the unshifted ALiBi scores (qb_transform's PRECISE form)
+        if (a.alibi && sv.lse && half == 0) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const int qrow = wq0 + 32 * qb + l32;
+                if (qrow < sv.Lq) sv.lse[qrow] -= rs[qb].slope * (float)row_dmin(rs[qb]);
+            }
+        }
+    }
 }
 
 // ----------------------------------------------------------------------------
