@@ -1,0 +1,118 @@
+"""Fixed-seed random sweep over the public API: shapes, head dims (8..128 and
+unpadded ones), GQA ratios, dense and varlen (with empty sequences), causal,
+windows, soft-cap, ALiBi, negative and small scales, every tile hint and
+split-KV chunk choice.  Deterministic (seeded), so it is an ordinary
+regression test with a wide net, not a fuzzer.
+
+Bars: fp32 within 1e-5 of the float64 restatement (oracle/stream_ref.c);
+bf16/fp16 within the north-star bars against the chunked oracle with a 1.25x
+allowance: a random draw lands on near-uniform rows (small or negative
+scales, D = 8, one row over ~10^3 keys), where O averages many values and the
+rounding of each probability to 16 bits before the PV product alone reaches
+~2^-9 of max|ref| (measured up to 1.2x the bars in such draws)."""
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+import mtlflashattn_amd as mfa
+from mtlflashattn_amd import _kernel
+from oracle import chunked
+from oracle.stream import stream_fwd
+from gpu_util import DEV, FP32_ATOL, REL_16, REL_16_OUT, make_qkv, make_varlen, max_err
+
+pytestmark = pytest.mark.gpu
+
+ALLOW = 1.25
+CASES = 160
+
+
+def _draw(i):
+    rng = random.Random(1000 + i)
+    dtype = rng.choice([torch.bfloat16, torch.float16, torch.bfloat16, torch.float32])
+    D = rng.choice([8, 16, 32, 40, 64, 64, 72, 96, 100, 128, 128, 33])
+    Hkv = rng.choice([1, 2, 4])
+    Hq = Hkv * rng.choice([1, 1, 2, 4])
+    kw = {}
+    if rng.random() < 0.5:
+        kw["causal"] = True
+    if rng.random() < 0.2:
+        kw["window_size"] = (rng.choice([0, 5, 64, 300]), rng.choice([-1, 0, 7, 100]))
+    if rng.random() < 0.25:
+        kw["softcap"] = rng.choice([3.0, 20.0])
+    if rng.random() < 0.25:
+        kw["alibi_slopes"] = [rng.uniform(0.0, 0.5) for _ in range(Hq)]
+    if rng.random() < 0.1:
+        kw["softmax_scale"] = rng.choice([0.05, 0.3, -0.1])
+    hint = rng.choice([0, 0, 1, 2, 3]) if dtype != torch.float32 else 0
+    split = rng.choice([None, None, 0, 64, 256]) if dtype != torch.float32 else None
+    if rng.random() < 0.35:
+        nb = rng.randint(1, 4)
+        lq = [rng.choice([0, 1, rng.randint(1, 40), rng.randint(1, 600)]) for _ in range(nb)]
+        lk = [rng.choice([0, 1, rng.randint(1, 70), rng.randint(1, 1300)]) for _ in range(nb)]
+        shape = ("varlen", lq, lk)
+    else:
+        shape = ("dense", rng.randint(1, 3), rng.choice([1, rng.randint(1, 64), rng.randint(1, 700)]),
+                 rng.choice([1, rng.randint(1, 64), rng.randint(1, 1500)]))
+    return dtype, D, Hq, Hkv, kw, hint, split, shape
+
+
+def _exact_dense(q, k, v, kw):
+    ws = kw.get("window_size", (-1, -1))
+    al = kw.get("alibi_slopes")
+    B, Hq = q.shape[0], q.shape[2]
+    return stream_fwd(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                      kw.get("softmax_scale", q.shape[-1] ** -0.5), kw.get("causal", False), kw.get("softcap", 0.0),
+                      ws[0], ws[1], alibi=al.repeat(B) if al is not None else None).transpose(1, 2)
+
+
+@pytest.mark.parametrize("i", range(CASES))
+def test_random_case(i, monkeypatch):
+    dtype, D, Hq, Hkv, kw, hint, split, shape = _draw(i)
+    if "alibi_slopes" in kw:
+        kw["alibi_slopes"] = torch.tensor(kw["alibi_slopes"], device=DEV)
+    monkeypatch.setattr(_kernel, "_TILE_HINT", hint)
+    monkeypatch.setattr(_kernel, "_SPLIT_KEYS", split)
+    cpu_kw = {a: (b.cpu() if torch.is_tensor(b) else b) for a, b in kw.items()}
+    what = f"case {i}: {dtype} D={D} Hq={Hq} Hkv={Hkv} hint={hint} split={split} {shape} {sorted(kw)}"
+    try:
+        if shape[0] == "varlen":
+            _, lq, lk = shape
+            q, k, v, cu_q, cu_k = make_varlen(lq, lk, Hq, Hkv, D, dtype, seed=i)
+            out = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lq + [1]), max(lk + [1]), **kw)
+            ref = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), **cpu_kw)
+            exact = None
+            if dtype == torch.float32:  # per sequence, as dense B=1 calls
+                exact = torch.zeros(out.shape, dtype=torch.float64)
+                sq = [0] + torch.tensor(lq).cumsum(0).tolist()
+                sk = [0] + torch.tensor(lk).cumsum(0).tolist()
+                for b in range(len(lq)):
+                    if lq[b] and lk[b]:
+                        exact[sq[b]:sq[b + 1]] = _exact_dense(q[None, sq[b]:sq[b + 1]], k[None, sk[b]:sk[b + 1]],
+                                                              v[None, sk[b]:sk[b + 1]], kw)[0]
+        else:
+            _, B, Lq, Lk = shape
+            q, k, v = make_qkv(B, Lq, Lk, Hq, Hkv, D, dtype, seed=i)
+            out = mfa.flash_attn_func(q, k, v, **kw)
+            ref = chunked.flash_attn_func(q.cpu(), k.cpu(), v.cpu(), **cpu_kw)
+            exact = _exact_dense(q, k, v, kw) if dtype == torch.float32 else None
+    except (NotImplementedError, RuntimeError) as e:  # a hint the shape does not admit
+        if "ping-pong" in str(e) or "tiles" in str(e) or "split" in str(e):
+            pytest.skip(str(e)[:80])
+        raise
+    if out.numel() == 0:
+        return
+    assert torch.isfinite(out).all(), what
+    if dtype == torch.float32:
+        assert (out.cpu().double() - exact).abs().max().item() <= FP32_ATOL, what
+        return
+    ref_max = max(ref.abs().max().item(), 1e-6)
+    assert max_err(out, ref) <= ALLOW * REL_16_OUT * ref_max, what
+    if shape[0] == "dense":
+        ws = kw.get("window_size", (-1, -1))
+        o32 = _kernel.forward_bshd(q, k, v, kw.get("softmax_scale", D ** -0.5), kw.get("causal", False),
+                                   kw.get("softcap", 0.0), ws[0], ws[1], kw.get("alibi_slopes"),
+                                   out_dtype=torch.float32)
+        assert max_err(o32, ref) <= ALLOW * REL_16 * ref_max, what
