@@ -122,6 +122,10 @@ constexpr int kWaves = 4;
 #ifndef MFA_PIPELINE
 #define MFA_PIPELINE 1
 #endif
+// head dims above 64 with ALiBi: walk the key blocks from the last to the first
+#ifndef MFA_ALIBI_REVERSE
+#define MFA_ALIBI_REVERSE 1
+#endif
 constexpr int kThreads = kWaves * 64;
 
 // ----------------------------------------------------------------------------
@@ -474,9 +478,6 @@ __device__ __forceinline__ void store_out(const KArgs& a, const SeqView& sv, f32
 // row-contiguous -- 16 lanes per 256-byte row -- instead of 32 rows in
 // 8-byte pieces per instruction.  The same values as store_out; the fp32
 // parity output keeps the direct store.
-#ifndef MFA_ALIBI_REVERSE
-#define MFA_ALIBI_REVERSE 1
-#endif
 #ifndef MFA_LDS_OSTORE
 #define MFA_LDS_OSTORE 1
 #endif
