@@ -106,10 +106,10 @@ constexpr int kWaves = 4;
 #ifndef MFA_PP_DMA_A
 #define MFA_PP_DMA_A 1
 #endif
-// ping-pong kernel at head dims up to 64: the row sums of a block's rounded
-// probabilities are issued at the start of the next MFMA phase (the softmax
-// phase is the longer one there, and dot2 instructions wait while the other
-// wavefront of the SIMD issues MFMAs, which it does not at that point) ...
+// ping-pong kernel: the row sums of a block's rounded probabilities are
+// issued at the start of the next MFMA phase (dot2 instructions wait while
+// the other wavefront of the SIMD issues MFMAs, which it does not at that
+// point) ...
 #ifndef MFA_PP_SUM_IN_A
 #define MFA_PP_SUM_IN_A 1
 #endif
@@ -1064,7 +1064,7 @@ template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4)))
 mfa_fwd16_pp_kernel(KArgs a) {
     static_assert(NW == 8 || NW == 16, "two or four wavefronts per SIMD");
-    constexpr bool SUM_IN_A = MFA_PP_SUM_IN_A && DP <= 64;
+    constexpr bool SUM_IN_A = MFA_PP_SUM_IN_A;
     constexpr int NT = NW * 64;        // threads
     constexpr int BM = NW * QB * 32;   // query rows per workgroup
     constexpr int BN = NKB * 32;       // keys per K/V block
