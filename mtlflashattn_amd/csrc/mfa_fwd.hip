@@ -86,9 +86,13 @@ constexpr int kWaves = 4;
 #ifndef MFA_PP_AHEAD
 #define MFA_PP_AHEAD 2
 #endif
-// the same for one query block per wavefront (one MFMA per fragment)
+// the same for one query block per wavefront (one MFMA per fragment), at
+// head dims up to 64 and above
 #ifndef MFA_PP_AHEAD1
 #define MFA_PP_AHEAD1 4
+#endif
+#ifndef MFA_PP_AHEAD1W
+#define MFA_PP_AHEAD1W 2
 #endif
 // raise the wave priority during the MFMA phase of the ping-pong kernel
 #ifndef MFA_PP_PRIO
@@ -1279,7 +1283,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
         constexpr int NPV = DB * NKB * 2;
         constexpr int NQK = NKB * DS;
         constexpr int NS = NPV + NQK;
-        constexpr int AH = NW == 16 ? MFA_PP_AHEAD16 : QB == 1 ? MFA_PP_AHEAD1 : MFA_PP_AHEAD;
+        constexpr int AH = NW == 16 ? MFA_PP_AHEAD16 : QB == 1 ? (DP > 64 ? MFA_PP_AHEAD1W : MFA_PP_AHEAD1) : MFA_PP_AHEAD;
         const uint16_t* vt = vst0 + ((u + NST - 1) % NST) * TILE;
         const uint16_t* kt = kst0 + (u % NST) * TILE;
         const uint16_t* kp[DS];
