@@ -82,6 +82,10 @@ constexpr int kWaves = 4;
 #ifndef MFA_SETPRIO
 #define MFA_SETPRIO 0
 #endif
+// ... and around the QK^T and PV MFMAs of a sequential block
+#ifndef MFA_SIMPLE_PRIO
+#define MFA_SIMPLE_PRIO 1
+#endif
 // fragments read ahead of their MFMAs in the ping-pong kernel's MFMA phase
 #ifndef MFA_PP_AHEAD
 #define MFA_PP_AHEAD 2
@@ -827,6 +831,7 @@ mfa_fwd16_kernel(KArgs a) {
     auto block_simple = [&](auto masked_tag, const uint16_t* kbuf, const uint16_t* vtb, int j) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         f32x16_t sacc[QB][NKB];
+        if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -840,6 +845,7 @@ mfa_fwd16_kernel(KArgs a) {
                 for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma16(kf, qf[qb][s], sacc[qb][kb]);
             }
         }
+        if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(0);
         u32x4_t pw[QB][NKB][2];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -848,6 +854,7 @@ mfa_fwd16_kernel(KArgs a) {
             if (qb_update(rs[qb], qb_max<NKB>(sacc[qb]), c, tau_c, alpha)) scale_rows<DB>(o[qb], alpha);
             qb_probs16<NKB, IS_BF16>(sacc[qb], pw[qb], rs[qb].l, rs[qb].mu, c);
         }
+        if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -859,6 +866,7 @@ mfa_fwd16_kernel(KArgs a) {
                     for (int qb = 0; qb < QB; ++qb)
                         o[qb][db] = mfma16(vf, __builtin_bit_cast(op_t, pw[qb][kb][st]), o[qb][db]);
                 }
+        if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
     // Software-pipelined unmasked block (QB >= 2).  Program order:
