@@ -105,3 +105,38 @@ def test_static_scratch_rejects_an_oversized_call():
     rc = lib.mfa_fwd_splitkv_static(ctypes.byref(p), 2048, None)
     assert rc == _hip.MFA_ERR_INVALID
     assert b"static scratch" in lib.mfa_last_error()
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_static_scratch_random_shapes(i):
+    # seeded draws over batch, query rows, key length, grouped-query ratio,
+    # head dim (padded and not), dtype, causal and chunk length (any multiple
+    # of 64): every call reuses the scratch the previous one left behind
+    import random
+    rng = random.Random(7000 + i)
+    B, Lq = rng.randint(1, 3), rng.choice([1, 2, 4, rng.randint(1, 64), rng.randint(1, 256)])
+    Lk, Hkv = rng.randint(100, 20000), rng.choice([1, 2, 4])
+    Hq, D = Hkv * rng.choice([1, 2, 4]), rng.choice([32, 40, 64, 96, 128])
+    causal, chunk = rng.random() < 0.5, 64 * rng.randint(1, 64)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    q, k, v = make_qkv(B, Lq, Lk, Hq, Hkv, D, dtype, seed=i)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for static in (True, False):
+        o = torch.full((B, Lq, Hq, D), float("nan"), dtype=torch.float32, device="cuda")
+        lse = torch.full((B, Hq, Lq), float("nan"), dtype=torch.float32, device="cuda")
+        p = params_bshd(q, k, v, o, causal, lse)
+        nbytes = _hip.workspace_bytes(p, chunk)
+        if not 0 < nbytes <= STATIC_SCRATCH_BYTES:
+            pytest.skip(f"workspace {nbytes} bytes is outside the static scratch")
+        if static:
+            _hip.fwd_splitkv_static(p, chunk, stream)
+        else:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+            _hip.fwd_splitkv(p, chunk, ws.data_ptr(), nbytes, stream)
+        torch.cuda.synchronize()
+        outs.append((o, lse))
+    (o_s, lse_s), (o_w, lse_w) = outs
+    what = f"case {i}: B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} D={D} causal={causal} chunk={chunk} {dtype}"
+    assert torch.isfinite(o_s).all(), what
+    assert torch.equal(o_s, o_w) and torch.equal(lse_s, lse_w), what
