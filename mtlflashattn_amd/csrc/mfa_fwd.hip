@@ -2239,21 +2239,36 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     // Auto: ping-pong tiles (512 rows at head dims <= 64, 256 at 128) when
     // they fill the chip (one workgroup per CU) and leave at most 25% more
     // rows empty than the 4-wavefront kernel's tiles (256 / 128 rows) do:
-    // short or single-row queries run faster on the 4-wavefront kernel.  At
-    // head dim 128 varlen and windowed calls stay on the 4-wavefront kernel
-    // too (measured: config 4 shapes 524 vs 559 us, config 5 861 vs 906).
+    // short or single-row queries run faster on the 4-wavefront kernel.
     const int64_t rows512 = (int64_t)((p->seqlen_q + 511) / 512) * 512;
     const int64_t rows256 = (int64_t)((p->seqlen_q + 255) / 256) * 256;
     const int64_t rows128 = (int64_t)((p->seqlen_q + 127) / 128) * 128;
     const int64_t units = (int64_t)p->batch * p->heads_q;
     bool fills_chip = pp_hint;
     if (p->tile_hint == MFA_TILE_AUTO) {
-        if (dp == 128)  // and rows long enough: >= 8 tiles per head, 16 when causal (measured:
-                        // B=32 Lq=256 44 vs 40 us, B=16 Lq=1024 causal 145 vs 116 on the ping-pong tiles)
-            fills_chip = !p->cu_seqlens_q && p->window_left < 0 && p->window_right < 0 &&
-                         units * (rows256 / 256) >= geom.cus && 4 * rows256 <= 5 * rows128 &&
-                         rows256 / 256 >= (p->causal ? 16 : 8);
-        else
+        if (dp == 128) {
+            // Rows long enough: >= 8 tiles per head, 16 when causal (measured:
+            // B=32 Lq=256 44 vs 40 us, B=16 Lq=1024 causal 145 vs 116 on the
+            // ping-pong tiles).  All 8 wavefronts of a ping-pong workgroup walk
+            // the key range of all its 256 rows, so a sliding window must be
+            // wide against that: windows of >= 2048 keys run 3-13% faster there
+            // (L=8192 (1024,1024) 145 vs 154 us, (4096,0) causal 234 vs 241,
+            // L=32768 (2048,0) causal 610 vs 634), narrower ones 7-10% slower
+            // ((256,256) 67 vs 61, (512,0) causal 67 vs 61).  A soft-cap /
+            // ALiBi transform under a window stays on the 4-wavefront kernel
+            // (config 5: 832 vs 791 us).  Varlen calls give only the longest
+            // sequence: the non-causal threshold rises to 12 tiles (config 4's
+            // lengths non-causal 798 vs 870 us; 32 lengths in [128, 2048] 828
+            // vs 751).
+            const int64_t t256 = rows256 / 256;
+            const int64_t inf = INT64_MAX / 4;
+            const int64_t left = p->window_left >= 0 ? p->window_left : inf;
+            const int64_t right = p->causal ? 0 : p->window_right >= 0 ? p->window_right : inf;
+            const bool windowed = p->window_left >= 0 || p->window_right >= 0;
+            const int64_t min_tiles = p->causal ? 16 : p->cu_seqlens_q ? 12 : 8;
+            fills_chip = units * t256 >= geom.cus && 4 * rows256 <= 5 * rows128 && t256 >= min_tiles &&
+                         (!windowed || (!bias && left + right + 1 >= 2048));
+        } else
             fills_chip = units * (rows512 / 512) >= geom.cus && 4 * rows512 <= 5 * rows256;
     }
     bool pp256 = p->tile_hint == MFA_TILE_PINGPONG256;

@@ -186,9 +186,19 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
     info = _kernel.launch_info(f16, f16, f16, causal=True)  # dense, 512 tiles of 256 rows: ping-pong
     assert info.kernel_name.startswith(b"mfa_fwd16pp<f16,d128") and info.rows_per_block == 256
-    # head dim 128: windowed calls and small grids stay on the 4-wavefront kernel
+    # head dim 128: narrow windows, windows under a soft-cap / ALiBi and small
+    # grids stay on the 4-wavefront kernel; windows of >= 2048 keys take the
+    # ping-pong tiles
     assert _kernel.launch_info(f16, f16, f16, window_left=256, window_right=256).kernel_name.startswith(
         b"mfa_fwd16<f16,d128")
+    assert _kernel.launch_info(f16, f16, f16, window_left=1024, window_right=1024).kernel_name.startswith(
+        b"mfa_fwd16pp<f16,d128")
+    assert _kernel.launch_info(f16, f16, f16, causal=True, window_left=4096, window_right=0).kernel_name.startswith(
+        b"mfa_fwd16pp<f16,d128")
+    assert _kernel.launch_info(f16, f16, f16, causal=True, window_left=1024, window_right=0).kernel_name.startswith(
+        b"mfa_fwd16<f16,d128")
+    assert _kernel.launch_info(f16, f16, f16, causal=True, softcap=30.0, window_left=4096,
+                               window_right=0).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     short128 = torch.empty(16, 1024, 16, 128, dtype=torch.float16)  # 4 tiles per head
     assert _kernel.launch_info(short128, short128, short128, causal=True).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     small128 = torch.empty(1, 2048, 16, 128, dtype=torch.float16)
@@ -200,6 +210,21 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     info = _kernel.launch_info(f32, f32, f32)
     assert info.kernel_name.startswith(b"mfa_fwd32<f32,d64")
     assert info.grid_x == 2 * (512 // info.rows_per_block)  # linear schedule: heads x tiles
+
+
+def test_varlen_d128_kernel_choice(lib):
+    # varlen calls give the longest sequence only: at head dim 128 the
+    # ping-pong tiles need >= 12 tiles of 256 rows non-causal, 16 causal
+    def varlen(nseq, longest, Hq, Hkv, causal):
+        p = good_params(B=nseq, L=longest, H=Hq, Hkv=Hkv, D=128)
+        p.q_batch_stride = p.k_batch_stride = p.v_batch_stride = p.o_batch_stride = 0
+        p.cu_seqlens_q = p.cu_seqlens_k = 256  # placeholder: planning reads no device memory
+        p.causal = int(causal)
+        return _hip.launch_info(p).kernel_name
+    assert varlen(8, 3501, 32, 8, False).startswith(b"mfa_fwd16pp<bf16,d128")
+    assert varlen(8, 3501, 32, 8, True).startswith(b"mfa_fwd16<bf16,d128")
+    assert varlen(32, 2048, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")
+    assert varlen(4, 8192, 16, 16, True).startswith(b"mfa_fwd16pp<bf16,d128")
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
