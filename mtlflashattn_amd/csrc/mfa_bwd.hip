@@ -869,6 +869,9 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     f.lse = p->softmax_lse;
     f.lse_b = p->lse_batch_stride;
     f.lse_h = p->lse_head_stride;
+    // (bounded before the int32 products below are formed)
+    if ((int64_t)p->batch * p->heads_q * (p->seqlen_q > 1 ? p->seqlen_q : 1) > 0x7fffffffLL)
+        return bset_err(MFA_ERR_INVALID, "mfa_bwd: problem too large");
     f.U = p->batch * p->heads_q;
     f.npages = 1;
     a.dout = static_cast<const char*>(bp->dout);

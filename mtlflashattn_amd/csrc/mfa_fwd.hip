@@ -2400,6 +2400,9 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
 
     const int rows = plan->cfg.rows;
     a.T = (p->seqlen_q + rows - 1) / rows;
+    // (bounded before the int32 product below is formed)
+    if ((int64_t)p->batch * p->heads_q * a.T > 0x7fffffffLL / 2)
+        return set_err(MFA_ERR_INVALID, "mfa_fwd: problem too large");
     a.U = p->batch * p->heads_q;
     const int64_t G = (int64_t)p->batch * p->heads_kv;
     const int X = geom.xcds;

@@ -227,6 +227,30 @@ def test_varlen_d128_kernel_choice(lib):
     assert varlen(4, 8192, 16, 16, True).startswith(b"mfa_fwd16pp<bf16,d128")
 
 
+def test_oversized_grids_are_rejected_not_wrapped(lib):
+    # batch * heads_q = 2^32 wraps a 32-bit product to 0 (an empty grid that
+    # would return OK without writing the output): both passes must reject it
+    p = good_params(B=65536, L=256, H=65536, Hkv=65536)
+    assert lib.mfa_fwd(ctypes.byref(p), None) == _hip.MFA_ERR_INVALID
+    assert b"too large" in lib.mfa_last_error()
+    info = _hip.MfaLaunchInfo()
+    assert lib.mfa_fwd_launch_info(ctypes.byref(p), ctypes.byref(info)) == _hip.MFA_ERR_INVALID
+    bp = _hip.MfaBwdParams()
+    bp.fwd = good_params(B=65536, L=256, H=65536, Hkv=65536)
+    bp.fwd.softmax_lse = 4096
+    bp.fwd.lse_batch_stride, bp.fwd.lse_head_stride = 65536 * 256, 256
+    for name, pre in (("dout", "do"), ("dq", "dq"), ("dk", "dk"), ("dv", "dv")):
+        setattr(bp, name, 4096)
+        setattr(bp, f"{pre}_batch_stride", bp.fwd.q_batch_stride)
+        setattr(bp, f"{pre}_seq_stride", bp.fwd.q_seq_stride)
+        setattr(bp, f"{pre}_head_stride", bp.fwd.q_head_stride)
+    bp.dtype_grad = _hip.MFA_DTYPE_BF16
+    assert lib.mfa_bwd_workspace_bytes(ctypes.byref(bp)) < 0
+    assert b"too large" in lib.mfa_last_error()
+    bp.fwd.batch, bp.fwd.heads_q, bp.fwd.heads_kv = 1, 4, 4  # the same call at a normal size plans
+    assert lib.mfa_bwd_workspace_bytes(ctypes.byref(bp)) > 0
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("MTLFLASHATTN_HIP_LIB", str(tmp_path / "nope.so"))
     monkeypatch.setattr(_hip, "_lib", None)
