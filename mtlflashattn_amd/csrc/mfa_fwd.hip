@@ -2429,7 +2429,8 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         a.nsplit = ns > 1 ? ns : 1;
         a.split_keys = split_keys;
         a.ws_ld = dp;
-        if ((int64_t)a.U * a.T * a.nsplit > 0x7fffffffLL / 2)
+        if ((int64_t)a.U * a.T * a.nsplit > 0x7fffffffLL / 2 ||
+            (int64_t)a.nsplit * a.U * p->seqlen_q > 0x7fffffffLL)  // (the merge grid: one workgroup per row)
             return set_err(MFA_ERR_INVALID, "mfa_fwd_splitkv: too many splits");
         a.T *= a.nsplit;
         plan->grid *= a.nsplit;
