@@ -1,0 +1,75 @@
+"""Head dim 128 calls that the automatic choice sends to the ping-pong tiles
+because their key ranges are long: sliding windows of >= 2048 keys without a
+soft-cap / ALiBi transform, and varlen calls whose longest sequence has >= 12
+tiles of 256 rows (16 when causal).  Each case checks the kernel the library
+picks (launch_info / the plan's name) and the result against the oracle
+(_kernel.py:1188-1207's mask order), in the fp32 parity
+output and the 16-bit output; the 4-wavefront kernel on the same call meets
+the same bars."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import mtlflashattn_amd as mfa
+from mtlflashattn_amd import _hip, _kernel
+from oracle import chunked
+from gpu_util import DEV, assert_output, assert_parity, default_scale, make_qkv, make_varlen
+
+pytestmark = pytest.mark.gpu
+
+DTYPES16 = [torch.bfloat16, torch.float16]
+
+
+def _fp32_dense(q, k, v, causal, ws):
+    return _kernel.forward_bshd(q, k, v, default_scale(q.shape[-1]), causal, 0.0, ws[0], ws[1], None,
+                                out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+@pytest.mark.parametrize("causal,ws,L,H", [
+    (False, (1024, 1023), 4096, 16),  # 2048 keys wide, both sides
+    (True, (2048, 0), 8192, 8),       # causal sliding window
+    (False, (2048, -1), 4096, 16),    # left bound only
+], ids=["both-sides", "causal", "left-only"])
+def test_wide_windows_take_the_pingpong_tiles(dtype, causal, ws, L, H, monkeypatch):
+    q, k, v = make_qkv(1, L, L, H, H, 128, dtype, seed=L + H + ws[0])
+    info = _kernel.launch_info(q, k, v, causal=causal, window_left=ws[0], window_right=ws[1])
+    assert info.kernel_name.startswith(b"mfa_fwd16pp<"), info.kernel_name
+    kw = dict(causal=causal, window_size=ws)
+    # the oracle on three 512-row chunks: the start (window not yet full),
+    # the middle and the end
+    starts = (0, L // 2, L - 512)
+    sel = torch.cat([torch.arange(s0, s0 + 512) for s0 in starts])
+    ref = chunked.flash_attn_func(q.cpu(), k.cpu(), v.cpu(), chunk=512, rows=set(starts), **kw)[:, sel]
+    assert_parity(_fp32_dense(q, k, v, causal, ws)[:, sel], ref, dtype, f"pp {ws} fp32 out")
+    assert_output(mfa.flash_attn_func(q, k, v, **kw)[:, sel], ref, dtype, f"pp {ws}")
+    monkeypatch.setattr(_kernel, "_TILE_HINT", _hip.MFA_TILE_256)  # the kernel these calls used before
+    assert_output(mfa.flash_attn_func(q, k, v, **kw)[:, sel], ref, dtype, f"4-wave {ws}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+def test_long_varlen_non_causal_takes_the_pingpong_tiles(dtype, monkeypatch):
+    lens = [3501, 2706, 3072, 400]  # longest: 14 tiles of 256 rows
+    q, k, v, cu_q, cu_k = make_varlen(lens, lens, 8, 2, 128, dtype, seed=44)
+    ran = []
+    orig = _kernel._launch
+
+    def spy(p, chunk, device):
+        ran.append(_hip.launch_info(p).kernel_name)
+        return orig(p, chunk, device)
+
+    monkeypatch.setattr(_kernel, "_launch", spy)
+    out = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens), max(lens))
+    assert ran and ran[-1].startswith(b"mfa_fwd16pp<"), ran
+    ref = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu())
+    assert_output(out, ref, dtype, "varlen non-causal (ping-pong)")
+    out32 = _kernel.forward_varlen(q, k, v, cu_q, cu_k, max(lens), max(lens), default_scale(128), False,
+                                   out_dtype=torch.float32)
+    assert_parity(out32, ref, dtype, "varlen non-causal fp32 out")
+    # causal: 14 tiles are below the causal threshold (16): 4-wavefront kernel
+    ran.clear()
+    outc = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens), max(lens), causal=True)
+    assert ran and ran[-1].startswith(b"mfa_fwd16<"), ran
+    refc = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=True)
+    assert_output(outc, refc, dtype, "varlen causal (4-wave)")
