@@ -17,9 +17,10 @@ Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
 Before the W warm-up steps the step also runs untimed for --clock-warmup
 seconds (default 1.0, declared in the line as clock_warmup_s/_steps) so that
 the K timed steps see the steady-state shader clock.
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7|8|9|10]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|4|5|6|7|8|9|10|11]
 (6-10: HBM-bound short-L, decode and tiny-key shapes, roofline in GB/s against
-8 TB/s; 8 runs split-KV)
+8 TB/s; 8 runs split-KV; 11: the fp32 path against the 157.3 TFLOP/s fp32
+MFMA peak)
 """
 from __future__ import annotations
 
@@ -148,6 +149,18 @@ def make_config(cfg: int):
                     algo=4 * pairs * D, varlen=None, hbm_bytes=2 * (2 * B * Lq * H * D + 2 * B * Lk * H * D),
                     workload=f"cfg10 (HBM-bound, not a BASELINE config): bf16 B={B} Lq={Lq} Lk={Lk} H={H} D={D} "
                              f"non-causal (tiny-key cross-attention), seed 10")
+    if cfg == 11:
+        # not a BASELINE config: the fp32 path (BASELINE config 1's dtype and
+        # head dim, at the headline sequence length; MFMA-bound on the fp32
+        # matrix cores, peak 157.3 TFLOP/s)
+        g = torch.Generator().manual_seed(11)
+        B, L, H, D = 1, 8192, 16, 64
+        q, k, v = (torch.randn(B, L, H, D, generator=g).to(dev) for _ in range(3))
+        pairs = B * H * L * L
+        return dict(q=q, k=k, v=v, kw=dict(causal=False), dtype="fp32", D=D, formula=4 * pairs * D,
+                    algo=4 * pairs * D, varlen=None,
+                    workload="cfg11 (fp32 path, not a BASELINE config): fp32 B=1 Lq=Lk=8192 H=16 D=64 non-causal, "
+                             "seed 11")
     raise SystemExit(f"unknown config {cfg}")
 
 
@@ -268,7 +281,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8, 9, 10],
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5, 6, 7, 8, 9, 10, 11],
                     help="BASELINE config 2-5 (default 2, the headline); 6-9 are HBM-bound short-L / decode "
                          "shapes (roofline in GB/s; 8 runs split-KV, 9 is grouped-query decode)")
     ap.add_argument("--clock-warmup", type=float, default=1.0,
