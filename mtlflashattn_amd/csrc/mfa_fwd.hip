@@ -1972,11 +1972,10 @@ KernelCfg cfg32(const char* name, bool paged) {
 #define MFA_STR2(...) #__VA_ARGS__
 #define MFA_STR(...) MFA_STR2(__VA_ARGS__)
 
-// bf16/fp16 head dims up to 64 use the ping-pong kernel (8 wavefronts,
-// 512-row tiles) when its tiles fill the chip.  (With one 32-query block per
-// wavefront, as a 128-wide head dim allows at two wavefronts per SIMD, every
-// K/V fragment feeds one MFMA and LDS bandwidth binds: measured slower than
-// the 4-wavefront kernel on the d128 configurations.)
+// bf16/fp16 calls use the ping-pong kernel (8 wavefronts) when its tiles fill
+// the chip (make_plan decides): 512-row tiles (two 32-row query blocks per
+// wavefront) or 256-row tiles (one) at head dims up to 64, 256-row tiles at
+// head dim 128.  Head dim 96 has no ping-pong tiles.
 #ifndef MFA_PINGPONG
 #define MFA_PINGPONG 1
 #endif
