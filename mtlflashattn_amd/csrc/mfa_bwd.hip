@@ -39,6 +39,14 @@
 
 namespace {
 
+// 32-row query sub-blocks per dK/dV step above head dim 64.  There the
+// kernel runs one wavefront per SIMD (K/V operands and dK/dV accumulators
+// resident), so each step's barrier, staging and LDS latency are exposed:
+// four sub-blocks (128 rows, 141 KB of LDS, no spills) amortise them over 4x
+// the MFMAs (config 3 backward 1.43 -> 1.26 ms, configs 4-5 -9 %; two: 1.30).
+#ifndef MFA_BWD_QSB_WIDE
+#define MFA_BWD_QSB_WIDE 4
+#endif
 constexpr int kBThreads = 256;  // 4 wavefronts
 
 struct BArgs {
@@ -272,10 +280,11 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     typedef Ops<IS_BF16> O;
     typedef typename O::op_t op_t;
     constexpr int DS = DP / 16, DB = DP / 32;
-    // query rows per step: QSB 32-row sub-blocks (two where the registers
-    // allow two wavefronts per SIMD with them: the per-step barrier, staging
-    // and lse/Dsum loads then serve twice the MFMAs)
-    constexpr int QSB = DP <= 64 ? 2 : 1;
+    // query rows per step: QSB 32-row sub-blocks (the per-step barrier,
+    // staging and lse/Dsum loads serve QSB times the MFMAs): two at head
+    // dims up to 64, where the registers allow two wavefronts per SIMD with
+    // them, MFA_BWD_QSB_WIDE above
+    constexpr int QSB = DP <= 64 ? 2 : MFA_BWD_QSB_WIDE;
     // At DP <= 64 (two wavefronts per SIMD, which hide the extra LDS read
     // before the first MFMA) Dsum is staged negated and dP starts from it, so
     // the accumulator ends as dP - Dsum; at larger DP Dsum is subtracted from
