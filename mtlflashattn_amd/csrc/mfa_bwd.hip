@@ -47,6 +47,10 @@ namespace {
 #ifndef MFA_BWD_QSB_WIDE
 #define MFA_BWD_QSB_WIDE 4
 #endif
+// 32-key blocks per dQ step
+#ifndef MFA_BWD_DQ_NKB
+#define MFA_BWD_DQ_NKB 2
+#endif
 constexpr int kBThreads = 256;  // 4 wavefronts
 
 struct BArgs {
@@ -291,6 +295,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     // the finished dP.
     constexpr bool DFOLD = DP <= 64;
     constexpr int BQ = 32 * QSB;
+    static_assert(BQ <= 128, "the host bounds a staged block's byte span for 128 rows");
     constexpr int QST = DP + 8;  // LDS row stride of the Q / dO tiles (elements)
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
     constexpr int SCH = (BQ * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread and tensor
@@ -568,7 +573,8 @@ mfa_bwd_dq_kernel(BArgs a) {
     typedef Ops<IS_BF16> O;
     typedef typename O::op_t op_t;
     constexpr int DS = DP / 16, DB = DP / 32;
-    constexpr int BN = 64, NKB = 2;  // keys per block
+    constexpr int NKB = MFA_BWD_DQ_NKB, BN = 32 * NKB;  // keys per block
+    static_assert(BN <= 128, "the host bounds a staged block's byte span for 128 rows");
     constexpr int KST = DP + 8;
     constexpr int CPR = DP / 8;
     constexpr int SCH = (BN * CPR + kBThreads - 1) / kBThreads;  // staged chunks per thread and tensor
@@ -839,11 +845,12 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
             return bset_err(MFA_ERR_INVALID, "mfa_bwd: alibi_batch_stride must be 0 or heads_q");
         if (p->lse_batch_stride < 0 || p->lse_head_stride < 0)
             return bset_err(MFA_ERR_INVALID, "mfa_bwd: lse strides must be >= 0");
-        // staged blocks (up to 64 rows) are addressed with 32-bit byte offsets
+        // staged blocks (up to 128 rows: the dK/dV kernel's query steps above
+        // head dim 64) are addressed with 32-bit byte offsets
         const int64_t rs[4] = {p->q_seq_stride, bp->do_seq_stride, p->k_seq_stride, p->v_seq_stride};
         for (int i = 0; i < 4; ++i)
-            if (rs[i] < 0 || (63 * rs[i] + D) * 2 >= ((int64_t)1 << 31))
-                return bset_err(MFA_ERR_INVALID, "mfa_bwd: sequence strides must be >= 0 and span < 2 GiB per 64 rows");
+            if (rs[i] < 0 || (127 * rs[i] + D) * 2 >= ((int64_t)1 << 31))
+                return bset_err(MFA_ERR_INVALID, "mfa_bwd: sequence strides must be >= 0 and span < 2 GiB per 128 rows");
     }
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128;
     const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);

@@ -251,6 +251,28 @@ def test_oversized_grids_are_rejected_not_wrapped(lib):
     assert lib.mfa_bwd_workspace_bytes(ctypes.byref(bp)) > 0
 
 
+def test_backward_rejects_strides_whose_128_row_span_overflows(lib):
+    # the dK/dV kernel stages 128 query rows per step above head dim 64: a
+    # query row stride of 10M elements spans < 2 GiB over 64 rows but not
+    # over 128, so the planner must reject it rather than wrap the offset
+    def bwd(qs):
+        bp = _hip.MfaBwdParams()
+        bp.fwd = good_params(B=1, L=256, H=4, Hkv=4, D=128)
+        bp.fwd.q_seq_stride = qs
+        bp.fwd.softmax_lse = 4096
+        bp.fwd.lse_batch_stride, bp.fwd.lse_head_stride = 4 * 256, 256
+        for name, pre in (("dout", "do"), ("dq", "dq"), ("dk", "dk"), ("dv", "dv")):
+            setattr(bp, name, 4096)
+            setattr(bp, f"{pre}_batch_stride", bp.fwd.k_batch_stride)
+            setattr(bp, f"{pre}_seq_stride", bp.fwd.k_seq_stride)
+            setattr(bp, f"{pre}_head_stride", bp.fwd.k_head_stride)
+        bp.dtype_grad = _hip.MFA_DTYPE_BF16
+        return lib.mfa_bwd_workspace_bytes(ctypes.byref(bp))
+    assert bwd(4 * 128) > 0
+    assert bwd(10_000_000) < 0
+    assert b"128 rows" in lib.mfa_last_error()
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("MTLFLASHATTN_HIP_LIB", str(tmp_path / "nope.so"))
     monkeypatch.setattr(_hip, "_lib", None)
