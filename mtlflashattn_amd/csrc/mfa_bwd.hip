@@ -47,6 +47,10 @@ namespace {
 #ifndef MFA_BWD_QSB_WIDE
 #define MFA_BWD_QSB_WIDE 4
 #endif
+// ... and at head dims up to 64 (two wavefronts per SIMD there)
+#ifndef MFA_BWD_QSB_NARROW
+#define MFA_BWD_QSB_NARROW 2
+#endif
 // 32-key blocks per dQ step
 #ifndef MFA_BWD_DQ_NKB
 #define MFA_BWD_DQ_NKB 2
@@ -288,7 +292,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     // staging and lse/Dsum loads serve QSB times the MFMAs): two at head
     // dims up to 64, where the registers allow two wavefronts per SIMD with
     // them, MFA_BWD_QSB_WIDE above
-    constexpr int QSB = DP <= 64 ? 2 : MFA_BWD_QSB_WIDE;
+    constexpr int QSB = DP <= 64 ? MFA_BWD_QSB_NARROW : MFA_BWD_QSB_WIDE;
     // At DP <= 64 (two wavefronts per SIMD, which hide the extra LDS read
     // before the first MFMA) Dsum is staged negated and dP starts from it, so
     // the accumulator ends as dP - Dsum; at larger DP Dsum is subtracted from
