@@ -43,15 +43,18 @@ namespace {
 // kernel runs one wavefront per SIMD (K/V operands and dK/dV accumulators
 // resident), so each step's barrier, staging and LDS latency are exposed:
 // four sub-blocks (128 rows, 141 KB of LDS, no spills) amortise them over 4x
-// the MFMAs (config 3 backward 1.43 -> 1.26 ms, configs 4-5 -9 %; two: 1.30).
+// the MFMAs (measured: fp16 B=1 L=8192 H=16 D=128 causal backward 1.43 ->
+// 1.26 ms, 1.30 with two; the bf16 D=128 varlen GQA and windowed soft-cap /
+// ALiBi shapes 9 % faster).
 #ifndef MFA_BWD_QSB_WIDE
 #define MFA_BWD_QSB_WIDE 4
 #endif
-// ... and at head dims up to 64 (two wavefronts per SIMD there)
+// ... and at head dims up to 64 (two wavefronts per SIMD there; four:
+// measured 35 % slower at bf16 B=1 L=8192 H=16 D=64)
 #ifndef MFA_BWD_QSB_NARROW
 #define MFA_BWD_QSB_NARROW 2
 #endif
-// 32-key blocks per dQ step
+// 32-key blocks per dQ step (four: measured 17 % slower at D=128)
 #ifndef MFA_BWD_DQ_NKB
 #define MFA_BWD_DQ_NKB 2
 #endif
