@@ -2255,10 +2255,11 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             // L=32768 (2048,0) causal 610 vs 634), narrower ones 7-10% slower
             // ((256,256) 67 vs 61, (512,0) causal 67 vs 61).  A soft-cap /
             // ALiBi transform under a window stays on the 4-wavefront kernel
-            // (config 5: 832 vs 791 us).  Varlen calls give only the longest
-            // sequence: the non-causal threshold rises to 12 tiles (config 4's
-            // lengths non-causal 798 vs 870 us; 32 lengths in [128, 2048] 828
-            // vs 751).
+            // (L=32768 H=16 causal (2048,0) with soft-cap 30 and ALiBi: 832 vs
+            // 791 us).  Varlen calls give only the longest sequence: the
+            // non-causal threshold rises to 12 tiles (8 lengths in [863, 3501]
+            // at Hq=32 Hkv=8: non-causal 798 vs 870 us; 32 lengths in
+            // [128, 2048]: 828 vs 751).
             const int64_t t256 = rows256 / 256;
             const int64_t inf = INT64_MAX / 4;
             const int64_t left = p->window_left >= 0 ? p->window_left : inf;
@@ -2303,8 +2304,8 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         // Windowed calls, causal calls with a soft-cap / ALiBi transform and
         // varlen calls run faster on the 4-wavefront kernel (measured at
         // L=8192 H=16 D=64: window (2048,0) 99 vs 106 us, (256,256) 45 vs
-        // 55, causal + soft-cap 261 vs 305; config 4's varlen lengths at
-        // D=64 Hq=32 Hkv=8: causal 306 vs 398 us, non-causal 512 vs 556): a
+        // 55, causal + soft-cap 261 vs 305; 8 varlen lengths in [863, 3501]
+        // at D=64 Hq=32 Hkv=8: causal 306 vs 398 us, non-causal 512 vs 556): a
         // ping-pong workgroup's waves share one K/V stream, so rows whose
         // window ends early wait through the rest of it, and 512-row tiles
         // leave much of a short sequence's last tile empty.
