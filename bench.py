@@ -9,8 +9,9 @@ one `flash_attn_func` forward over inputs already resident in HBM.
 
 Prints ONE JSON line (rank 0).  Besides the driver's fields it carries
   roofline     : the dominant kernel's algorithmic FLOPs / its average launch
-                 time (HIP events around each launch on the launch stream),
-                 against the dense bf16 MFMA peak (2.5 PFLOP/s);
+                 time (HIP events over the K back-to-back timed launches, on
+                 the launch stream), against the dense bf16 MFMA peak
+                 (2.5 PFLOP/s);
   cpu_baseline : the reference's chunked-fp32 torch path (oracle/chunked.py)
                  timed on this host's cores on a bounded sample of the same
                  workload (a subset of heads).
@@ -341,14 +342,15 @@ def main():
     torch.cuda.synchronize()
     ms_total = t_start.elapsed_time(t_end)
     ms_step = ms_total / args.steps
-    # per-launch kernel time: events bracketing each launch on its stream
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for a, b in evs:
-        a.record(stream)
-        step()
-        b.record(stream)
-    torch.cuda.synchronize()
-    kernel_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    # Kernel time per launch: the same HIP event pair over the K back-to-back
+    # steps, on the stream the kernels are launched on.  The host queues the
+    # steps faster than the GPU runs them, so the GPU runs the kernels back to
+    # back and this is their average duration (plus the dispatch gap between
+    # consecutive kernels).  A forward step is one launch; split-KV (config 8)
+    # adds the merge kernel and --backward runs three kernels, whose sum this
+    # is.  (Events bracketing each call separately would add the event
+    # records' own cost to every launch.)
+    kernel_ms = ms_step
 
     value = c["formula"] / (ms_step / 1e3) / 1e12
     peak = PEAK_TFLOPS[c["dtype"]]
@@ -389,14 +391,16 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kname,
                      "kernel_ms": round(kernel_ms, 4),
-                     "note": "algorithmic FLOPs (4*D per valid (query,key) pair) / mean launch time"},
+                     "note": "algorithmic FLOPs (4*D per valid (query,key) pair) / mean launch time "
+                             "(HIP events over the K back-to-back timed launches)"},
     }
     if "hbm_bytes" in c:
         gbs = c["hbm_bytes"] / (kernel_ms / 1e3) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kname,
                             "kernel_ms": round(kernel_ms, 4), "algorithmic_bytes": c["hbm_bytes"],
-                            "note": "algorithmic bytes (Q + K + V + O, each once) / mean launch time"}
+                            "note": "algorithmic bytes (Q + K + V + O, each once) / mean launch time "
+                                    "(HIP events over the K back-to-back timed launches)"}
     if args.copy_calibration:
         x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
         y = torch.empty_like(x)

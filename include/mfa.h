@@ -23,8 +23,11 @@
  *    from mfa_last_error() on the same thread.
  *  - All pointers are device pointers.  The head dimension must be
  *    contiguous (element stride 1) in q, k, v and o; every other stride is an
- *    element stride and may be arbitrary (views, packed qkv, heads-second or
- *    heads-third layouts).
+ *    element stride and may describe any layout (views, packed qkv,
+ *    heads-second or heads-third), as long as q, k, v and o start at 16-byte
+ *    aligned addresses and each of their strides is a multiple of 16 bytes
+ *    (8 elements of 16 bits, 4 of fp32); other layouts return
+ *    MFA_ERR_INVALID.
  */
 #ifndef MTLFA_MFA_H
 #define MTLFA_MFA_H
@@ -76,6 +79,10 @@ extern "C" {
  *   [cu_seqlens_k[i], cu_seqlens_k[i+1]) of k/v.  `batch` is the number of
  *   sequences, the *_batch_stride fields are ignored, and seqlen_q/seqlen_k
  *   must hold max_seqlen_q/max_seqlen_k (upper bounds of every sequence).
+ *   The kernel and tile choice is made from these bounds (e.g. seqlen_k <= 32
+ *   under many query rows selects a kernel that holds one 32-key block per
+ *   sequence), so a bound below a sequence's real length gives wrong
+ *   results for that sequence; it is not detected on the device.
  *
  * Masking/bias (metal_flash_attn/_kernel.py:32-87): for query row i of a
  * sequence with Lq queries and Lk keys, center = i + (Lk - Lq); key j is
@@ -142,7 +149,9 @@ typedef struct mfa_fwd_params {
      * key count of sequence b is seqlen_k (dense) or cu_seqlens_k[b+1] -
      * cu_seqlens_k[b] (varlen; the start offsets are not used for k/v).
      * page_block_size is a positive multiple of 256; a page id outside
-     * [0, num_pages) reads as zeros (callers validate their tables).  Paged
+     * [0, num_pages) reads as zeros, never out of bounds, but its keys are
+     * not masked: they score 0 and take weight in the softmax, so the rows
+     * that see them come out wrong (callers validate their tables).  Paged
      * calls run on the 256-row and fp32 kernels: MFA_TILE_PINGPONG with a
      * block_table is MFA_ERR_UNSUPPORTED. */
     const int32_t* block_table; /* NULL = contiguous k/v */

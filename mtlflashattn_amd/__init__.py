@@ -157,7 +157,11 @@ def flash_attn_varlen_func(
     [B, max_pages]; k, v are then page pools [num_pages, page_block_size, Hkv,
     D] with page_block_size a multiple of 256, key j of sequence b is row
     j % page_block_size of page block_table[b, j // page_block_size], and
-    cu_seqlens_k gives the key counts only.
+    cu_seqlens_k gives the key counts only.  Page ids are read on the device;
+    an id outside [0, num_pages) reads zero keys and values without faulting,
+    but those keys are not masked (they score 0 and dilute the softmax), so
+    the rows that see them are wrong; MTLFLASHATTN_CHECK_PAGES=1 checks the
+    ids on the host and raises ValueError instead.
     """
     _check_supported(q, k, v, dropout_p, window_size, softcap, alibi_slopes, deterministic, return_attn_probs)
     return _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_size, softcap, alibi_slopes,

@@ -185,6 +185,21 @@ def _fits_abi(x: torch.Tensor) -> bool:
     return all(st % al == 0 for st, n in zip(x.stride()[:-1], x.shape[:-1]) if n > 1)
 
 
+def _abi_operand(x: torch.Tensor) -> torch.Tensor:
+    """x itself when it meets the C ABI's layout rule (_fits_abi), else a
+    fresh contiguous copy.  A contiguous tensor at a storage offset that is
+    not 16-byte aligned (e.g. base[1:].view(...)) stays misaligned under
+    .contiguous(), which returns it unchanged; a new allocation from torch's
+    caching allocator is aligned."""
+    if _fits_abi(x):
+        return x
+    y = x.contiguous()
+    if y is x or not _fits_abi(y):
+        y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        y.copy_(x)
+    return y
+
+
 def _strides_bsh(x: torch.Tensor):
     """(batch, seq, head) element strides of a [B, S, H, D] view; 0 for size-1 dims."""
     return tuple(int(st) if n > 1 else 0 for st, n in zip(x.stride()[:3], x.shape[:3]))
@@ -249,7 +264,7 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
             return out
     if Dp != D:  # the kernels read 16-byte chunks: zero-pad the head dim
         q, k, v = (F.pad(t, (0, Dp - D)) for t in (q, k, v))
-    q, k, v = (t if _fits_abi(t) else t.contiguous() for t in (q, k, v))
+    q, k, v = (_abi_operand(t) for t in (q, k, v))
     dst = out
     if Dp != D or not _fits_abi(out) or out.stride(-1) != 1:
         dst = torch.empty(out.shape[:-1] + (Dp,), dtype=out.dtype, device=out.device)
@@ -511,7 +526,7 @@ def _run_bwd(q, k, v, out, dout, lse, *, scale, causal, softcap, window_left, wi
     ts = [q, k, v, out, dout.to(q.dtype)]
     if Dp != D:
         ts = [F.pad(t, (0, Dp - D)) for t in ts]
-    q_, k_, v_, o_, do_ = (t if _fits_abi(t) else t.contiguous() for t in ts)
+    q_, k_, v_, o_, do_ = (_abi_operand(t) for t in ts)
     dq = torch.empty(q_.shape, dtype=gdt, device=q.device)
     dk = torch.empty(k_.shape, dtype=gdt, device=q.device)
     dv = torch.empty(v_.shape, dtype=gdt, device=q.device)

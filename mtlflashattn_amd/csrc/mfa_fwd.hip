@@ -2213,9 +2213,13 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             if (s_in[i] % in_al != 0)
                 return set_err(MFA_ERR_INVALID, "mfa_fwd: q/k/v strides must be multiples of %lld elements",
                                (long long)in_al);
-        const int64_t out_al = oes == 4 ? 4 : 4;  // 4-element (8 or 16 byte) stores
+        // O leaves the 16-bit kernels in row-contiguous 16-byte pieces (and a
+        // packed grouped-query decode uses the head stride as its row stride),
+        // so every o stride is a multiple of 16 bytes, as for q/k/v
+        const int64_t out_al = 16 / oes;
         if (p->o_batch_stride % out_al || p->o_seq_stride % out_al || p->o_head_stride % out_al)
-            return set_err(MFA_ERR_INVALID, "mfa_fwd: o strides must be multiples of 4 elements");
+            return set_err(MFA_ERR_INVALID, "mfa_fwd: o strides must be multiples of %lld elements (16 bytes)",
+                           (long long)out_al);
         if (p->alibi_slopes && !(p->alibi_batch_stride == 0 || p->alibi_batch_stride == p->heads_q))
             return set_err(MFA_ERR_INVALID, "mfa_fwd: alibi_batch_stride must be 0 or heads_q");
     }

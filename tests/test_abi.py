@@ -86,6 +86,13 @@ def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
     (lambda p: setattr(p, "window_left", -2), _hip.MFA_ERR_INVALID, "window"),
     (lambda p: setattr(p, "q", 4098), _hip.MFA_ERR_INVALID, "aligned"),
     (lambda p: setattr(p, "k_seq_stride", 68), _hip.MFA_ERR_INVALID, "strides"),
+    # 16-bit O is stored in 16-byte row pieces: o strides of 4 (not 8) elements are refused
+    (lambda p: setattr(p, "o_seq_stride", 4 * 64 + 4), _hip.MFA_ERR_INVALID, "o strides"),
+    # a padded o head stride (D + 4) on a single-row grouped-query decode, whose
+    # packed rows are addressed through the head stride
+    (lambda p: (setattr(p, "seqlen_q", 1), setattr(p, "heads_kv", 1), setattr(p, "o_head_stride", 68),
+                setattr(p, "o_seq_stride", 4 * 68), setattr(p, "o_batch_stride", 4 * 68)),
+     _hip.MFA_ERR_INVALID, "o strides"),
     (lambda p: setattr(p, "o", None), _hip.MFA_ERR_INVALID, "NULL"),
     (lambda p: setattr(p, "cu_seqlens_q", 256), _hip.MFA_ERR_INVALID, "cu_seqlens"),
     (lambda p: setattr(p, "tile_hint", 4), _hip.MFA_ERR_INVALID, "tile_hint"),

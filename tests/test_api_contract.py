@@ -307,3 +307,50 @@ def test_kernel_mode_env_selects_the_single_path(monkeypatch, fake_device):
     _kernel._warned_modes.clear()
     with pytest.warns(UserWarning, match="single HIP"):
         assert _kernel._kernel_mode() == "hip"
+
+
+class TestLauncherAlignment:
+    """The C ABI takes 16-byte aligned bases and strides (include/mfa.h).  The
+    reference has no alignment rule (metal_flash_attn/_kernel.py:1296-1298),
+    so the launcher must copy a legal tensor that breaks it, including a
+    contiguous one at a misaligned storage offset, where .contiguous() is a
+    no-op."""
+
+    @staticmethod
+    def recorded_launch(monkeypatch):
+        launches = []
+
+        def fake_launch(p, chunk, device):
+            launches.append(p)
+
+        monkeypatch.setattr(_kernel, "_launch", fake_launch)
+        monkeypatch.setattr(_kernel, "_split_choice", lambda p, dtype, hint: 0)
+        _kernel._plans.clear()
+        return launches
+
+    def test_misaligned_contiguous_inputs_are_copied(self, monkeypatch):
+        B, L, H, D = 2, 16, 4, 64
+        base = torch.randn(1 + B * L * H * D, dtype=torch.float32).to(torch.bfloat16)
+        q = base[1:].view(B, L, H, D)
+        assert q.is_contiguous() and q.data_ptr() % 16 == 2 and q.contiguous() is q
+        fixed = _kernel._abi_operand(q)
+        assert fixed.data_ptr() % 16 == 0 and torch.equal(fixed, q)
+        assert _kernel._abi_operand(fixed) is fixed  # aligned tensors pass through uncopied
+
+        launches = self.recorded_launch(monkeypatch)
+        out = torch.empty(B, L, H, D, dtype=torch.bfloat16)
+        _kernel._run(q, q, q, out, scale=0.125, causal=False, softcap=0.0, window_left=-1, window_right=-1,
+                     alibi=None, alibi_bstride=0)
+        p = launches[-1]
+        assert p.q % 16 == 0 and p.k % 16 == 0 and p.v % 16 == 0 and p.o % 16 == 0
+        assert (p.q_seq_stride, p.q_head_stride) == (H * D, D)
+
+    def test_misaligned_output_goes_through_a_staging_buffer(self, monkeypatch):
+        B, L, H, D = 1, 8, 2, 32
+        q = torch.zeros(B, L, H, D, dtype=torch.float16)
+        obase = torch.zeros(1 + B * L * H * D, dtype=torch.float16)
+        out = obase[1:].view(B, L, H, D)
+        launches = self.recorded_launch(monkeypatch)
+        _kernel._run(q, q, q, out, scale=0.125, causal=False, softcap=0.0, window_left=-1, window_right=-1,
+                     alibi=None, alibi_bstride=0)
+        assert launches[-1].o % 16 == 0 and launches[-1].o != out.data_ptr()

@@ -141,6 +141,23 @@ class TestFlashAttnFunc:
         q = base.transpose(1, 2)  # heads-third view with heads-second strides
         check(q, q, q, "transposed view")
 
+    @pytest.mark.parametrize("dtype", DTYPES)
+    def test_misaligned_contiguous_inputs(self, dtype):
+        # contiguous tensors at storage offsets that are not 16-byte aligned
+        # (.contiguous() returns them unchanged): the launcher copies them
+        # (the reference has no alignment rule, metal_flash_attn/_kernel.py:1296-1298)
+        B, L, H, D = 2, 96, 4, 64
+        g = torch.Generator().manual_seed(21)
+        n = B * L * H * D
+        base = torch.randn(3 * n + 3, generator=g).to("cuda", dtype)
+        q = base[1:1 + n].view(B, L, H, D)
+        k = base[2 + n:2 + 2 * n].view(B, L, H, D)
+        v = base[3 + 2 * n:3 + 3 * n].view(B, L, H, D)
+        assert q.is_contiguous() and q.data_ptr() % 16 != 0
+        check(q, k, v, "misaligned", causal=True)
+        assert torch.equal(mfa.flash_attn_func(q, k, v, causal=True),
+                           mfa.flash_attn_func(q.clone(), k.clone(), v.clone(), causal=True))
+
 
 @pytest.mark.usefixtures("tile")
 class TestFeatures:

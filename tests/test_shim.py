@@ -112,7 +112,7 @@ def test_install_is_idempotent():
         import _mtlflashattn_amd_finder as f
         import mtlflashattn_amd._shim as s
         assert f.install() is False and s.install() is False
-        n = sum(isinstance(x, f._MtlFlashAttnAmdFinder) for x in __import__("sys").meta_path)
+        n = sum(isinstance(x, f.FlashAttnAlias) for x in __import__("sys").meta_path)
         print(n)
     """)
     assert r.returncode == 0, r.stderr
@@ -132,6 +132,44 @@ def test_packages_distributions_consistency():
     """)
     assert r.returncode == 0, r.stderr
     assert r.stdout.strip() == "2.7.4"
+
+
+def test_metadata_record_answers_version_lookups():
+    # the provider record is an ordinary discovered distribution: version()
+    # and the name lookup resolve through it in a source tree
+    r = run_py("""
+        import _mtlflashattn_amd_finder, importlib.metadata as md
+        from mtlflashattn_amd._version import __version__
+        assert md.version("mtlflashattn_amd") == __version__, md.version("mtlflashattn_amd")
+        assert md.distribution("mtlflashattn-amd").metadata["Name"] == "mtlflashattn_amd"
+        assert md.packages_distributions()["flash_attn"] == ["mtlflashattn_amd"]
+        print("ok")
+    """)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "ok"
+
+
+def test_real_install_keeps_the_metadata_mapping(tmp_path):
+    # with a real flash_attn importable the hook contributes no record, so the
+    # mapping holds only what the real install declares (here: nothing)
+    pkg = tmp_path / "real" / "flash_attn"
+    pkg.mkdir(parents=True)
+    (pkg / "__init__.py").write_text('__version__ = "9.9.9-real"\n')
+    r = run_py("""
+        import _mtlflashattn_amd_finder, importlib.metadata as md
+        print("flash_attn" in md.packages_distributions())
+    """, pythonpath=str(tmp_path / "real"))
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "False"
+
+
+def test_kill_switch_removes_the_metadata_record():
+    r = run_py("""
+        import _mtlflashattn_amd_finder, importlib.metadata as md
+        print("flash_attn" in md.packages_distributions())
+    """, env_extra={"MTLFLASHATTN_SHIM": "off"})
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "False"
 
 
 def test_shimmed_call_reaches_the_contract():
