@@ -53,7 +53,10 @@ extern "C" {
 
 #define MFA_MAX_HEAD_DIM 128
 
-/* tile_hint values (bf16/fp16 only; fp32 has one kernel) */
+/* tile_hint values (bf16/fp16 only; fp32 has one kernel).  Sequences of one
+ * query row (and single-row grouped-query decode, whose query heads are
+ * computed as the rows of one K/V head) always run the exact-row kernel,
+ * whose probabilities carry two 16-bit terms; the hint applies to the rest. */
 #define MFA_TILE_AUTO 0     /* library's choice */
 #define MFA_TILE_256 1      /* 256-row tiles, 4 wavefronts */
 #define MFA_TILE_PINGPONG 2 /* ping-pong tiles, 8 wavefronts: 512 rows at head_dim <= 64,
@@ -126,7 +129,8 @@ typedef struct mfa_fwd_params {
     int32_t dtype_in;  /* MFA_DTYPE_* of q, k and v */
     int32_t dtype_out; /* == dtype_in, or MFA_DTYPE_F32 (full-precision output) */
     int32_t tile_hint; /* MFA_TILE_AUTO (0); the others force a bf16/fp16 kernel
-                          (tests and tuning; results are the same either way) */
+                          (tests and tuning; results meet the same bars either
+                          way) for every sequence of more than one query row */
 
     /* Softmax log-sum-exp output (optional; the reference raises for it,
      * metal_flash_attn/__init__.py:49-50).  lse = ln(sum_j exp(s_j)) over the

@@ -57,6 +57,11 @@ struct KArgs {
     // packed, else 1; rows then step by qs / os)
     int64_t qts, ots;
     int32_t pack_r;
+    // sequences of one query row (varlen calls that mix them with longer
+    // ones): 0 = every sequence is this launch's, 1 = this launch skips them
+    // (the exact-row kernel's launch computes them), 2 = this launch (the
+    // exact-row kernel) computes only them
+    int32_t single_rows;
     int32_t out_f32;
     // schedule
     int32_t T;        // query tiles per (sequence, head)

@@ -412,6 +412,44 @@ __device__ __forceinline__ float qb_sum16(const u32x4_t (&pw)[NKB][2]) {
     return acc[0] + acc[1];
 }
 
+// Two-term 16-bit probabilities, for rows whose O averages so many
+// near-equal weights that one 16-bit rounding of each weight is visible
+// against max|O| (single-row sequences and packed grouped-query decode rows):
+// hi = round16(p) and lo = round16(p - hi) (the difference is exact in fp32).
+// The PV MFMA consumes both against the same V fragment, so the weights carry
+// about 16 mantissa bits instead of 8 (bf16) or 11 (fp16).  The row sum adds
+// the fp32 weights themselves (two chains, acc[0] and acc[1]), which hi + lo
+// reproduce to 2^-17 relative (plain adds: two dot2 per pair measured 1.2%
+// slower on single-row decode).
+// One group: the 8 weights of accumulator registers 8*st..8*st+7.
+template <bool IS_BF16>
+__device__ __forceinline__ void probs16x2_group(const f32x16_t& s, int st, u32x4_t& ph, u32x4_t& pl,
+                                                float (&acc)[2], float mu, float c) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float p0 = fast_exp2(fmaf(s[8 * st + 2 * w], c, -mu));
+        const float p1 = fast_exp2(fmaf(s[8 * st + 2 * w + 1], c, -mu));
+        float h0, h1;
+        if constexpr (IS_BF16) {
+            const bf16x2_t hk = {(__bf16)p0, (__bf16)p1};
+            const uint32_t h = __builtin_bit_cast(uint32_t, hk);
+            h0 = __builtin_bit_cast(float, h << 16);
+            h1 = __builtin_bit_cast(float, h & 0xffff0000u);
+            const bf16x2_t lk = {(__bf16)(p0 - h0), (__bf16)(p1 - h1)};
+            ph[w] = h;
+            pl[w] = __builtin_bit_cast(uint32_t, lk);
+        } else {
+            const f16x2_t hk = {(_Float16)p0, (_Float16)p1};
+            h0 = (float)hk[0];
+            h1 = (float)hk[1];
+            const f16x2_t lk = {(_Float16)(p0 - h0), (_Float16)(p1 - h1)};
+            ph[w] = __builtin_bit_cast(uint32_t, hk);
+            pl[w] = __builtin_bit_cast(uint32_t, lk);
+        }
+        acc[w & 1] += p0 + p1;
+    }
+}
+
 template <int NKB>
 __device__ __forceinline__ void qb_probs32(f32x16_t (&s)[NKB], float& l, float mu, float c) {
     float acc[2] = {0.f, 0.f};
@@ -638,11 +676,15 @@ __global__ void __launch_bounds__(64) mfa_combine_kernel(KArgs a) {
 //   DP  : head dim padded to a multiple of 32 (32, 64, 96, 128)
 //   QB  : 32-query column blocks per wavefront (workgroup rows = 4*32*QB)
 //   NKB : 32-key row blocks per K/V block (keys per block = 32*NKB)
+//   EXACT: the exact-row instantiation (block_exact below): the kernel of
+//          single-row sequences and packed grouped-query decode rows.  It is
+//          a separate kernel, not a path of the others: a second block path
+//          inside their key loop made the register allocator spill in it.
 // With QB >= 2, unmasked blocks run software-pipelined: the QK^T MFMAs of
 // query block qb+1 and the PV MFMAs of query block qb-1 are interleaved with
 // the softmax VALU work of query block qb, so the matrix cores and the
 // vector ALU run concurrently within one wavefront.
-template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, bool PAGED>
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, bool PAGED, bool EXACT>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MFA_WAVES_PER_EU)))
 mfa_fwd16_kernel(KArgs a) {
     constexpr int BM = kWaves * QB * 32;
@@ -657,7 +699,13 @@ mfa_fwd16_kernel(KArgs a) {
     constexpr int V_ELEMS = BN * VST;
     constexpr int KV_ELEMS = 2 * (K_ELEMS + V_ELEMS);
     constexpr int Q_ELEMS = BM * KST;
-    constexpr int SMEM = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+    // The exact-row kernel's LDS is sized (at least 60 KB) so that two
+    // workgroups share a CU, as with the other kernels' tiles: its decode
+    // workgroups are HBM-streaming, and three per CU at head dim 64 (what
+    // its registers and 43 KB of K/V stages would allow) measured 18% slower
+    // than two (B=64 H=16 Lk=4096 D=64 single rows: 0.238 against 0.201 ms).
+    constexpr int SMEM_KV = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+    constexpr int SMEM = (EXACT && SMEM_KV < 30000) ? 30000 : SMEM_KV;
     constexpr int CPR = DP / 8;                                 // 16-byte chunks per row
     constexpr int KCH = (BN * CPR + kThreads - 1) / kThreads;  // chunks per thread per tile
     typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
@@ -674,6 +722,9 @@ mfa_fwd16_kernel(KArgs a) {
     const SeqView sv = seq_view<2>(a, b, hq);
     const int q0 = tile * BM;
     if (q0 >= sv.Lq) return;
+    // a varlen call mixing single-row sequences with longer ones: the
+    // exact-row kernel's launch takes the single-row ones, this one the rest
+    if (a.single_rows != 0 && (sv.Lq == 1) != EXACT) return;
     // split-KV: this sequence's chunks (one when it has no key)
     if (a.nsplit > 1 && split >= max(1, (sv.Lk + a.split_keys - 1) / a.split_keys)) return;
 
@@ -704,10 +755,13 @@ mfa_fwd16_kernel(KArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.f;
     const float c = BIAS ? kLog2e : a.scale_log2;
-    // exact (per-row) rescales for single-row sequences and packed
-    // grouped-query decode rows: their results do not depend on which rows
-    // share a wave, so packed heads equal unpacked ones bit for bit
-    const float tau = (Lq == 1 || a.decode_pack) ? 0.f : (float)MFA_RESCALE_TAU;
+    // Exact rows (this instantiation's: single-row sequences and packed
+    // grouped-query decode rows) take per-row rescales -- their results do not
+    // depend on which rows share a wave, so packed heads equal unpacked ones
+    // bit for bit -- and two-term probabilities (block_exact): a single row
+    // averaging thousands of near-equal weights has a small max|O|, against
+    // which one 16-bit rounding of every weight is visible.
+    const float tau = (EXACT || Lq == 1 || a.decode_pack) ? 0.f : (float)MFA_RESCALE_TAU;
     const float tau_c = tau / c;
 
     // ---- key range of the workgroup and of this wavefront
@@ -869,6 +923,59 @@ mfa_fwd16_kernel(KArgs a) {
         if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
+    // Block of the exact-row instantiation: query blocks one at a time, each
+    // skipped when it holds no row of the sequence (a single query row leaves
+    // every block but the wave's first empty), with two-term probabilities
+    // and two PV MFMAs per V fragment (probs16x2_group).
+    auto block_exact = [&](auto masked_tag, const uint16_t* kbuf, const uint16_t* vtb, int j) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            if (wq0 + 32 * qb >= Lq) break;  // (wave-uniform)
+            f32x16_t sacc[NKB];
+            if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+                for (int s = 0; s < DS; ++s) {
+                    const op_t kf = *reinterpret_cast<const op_t*>(kbuf + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                    sacc[kb] = mfma16(kf, qf[qb][s], sacc[kb]);
+                }
+            }
+            if constexpr (MFA_SIMPLE_PRIO) __builtin_amdgcn_s_setprio(0);
+            qb_transform<NKB, BIAS, MASKED>(a, sacc, rs[qb], j, half);
+            float alpha;
+            if (qb_update(rs[qb], qb_max<NKB>(sacc), c, tau_c, alpha)) scale_rows<DB>(o[qb], alpha);
+            // each group of 8 weights goes to the PV MFMAs right after it is
+            // formed, so the scores free their registers group by group (the
+            // lo terms would not fit beside all of them at head dim 128);
+            // every O row block still sees the k-steps in the order
+            // (kb, st), hi before lo
+            float acc[2] = {0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    // (fenced, so the scheduler does not hoist every group's V
+                    // fragment reads to the top, which would hold them all in
+                    // registers at once)
+                    __builtin_amdgcn_sched_barrier(0);
+                    u32x4_t ph, pl;
+                    probs16x2_group<IS_BF16>(sacc[kb], st, ph, pl, acc, rs[qb].mu, c);
+#pragma unroll
+                    for (int db = 0; db < DB; ++db) {
+                        const op_t vf = load_vf(vtb, db, kb, st);
+                        o[qb][db] = mfma16(vf, __builtin_bit_cast(op_t, ph), o[qb][db]);
+                        o[qb][db] = mfma16(vf, __builtin_bit_cast(op_t, pl), o[qb][db]);
+                    }
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            rs[qb].l += acc[0] + acc[1];
+        }
+    };
+
     // Software-pipelined unmasked block (QB >= 2).  Program order:
     //   QK(0) | QK(1) + softmax(0) | PV(0) + softmax(1) | ... | PV(QB-1)
     // where "+" means the MFMAs are issued one or two at a time between the
@@ -1014,7 +1121,15 @@ mfa_fwd16_kernel(KArgs a) {
         const bool masked = !((j >= w_lo_last) && (j + BN - 1 <= w_hi_first));
         const uint16_t* kbuf = smem + buf * K_ELEMS;
         const uint16_t* vtb = smem + 2 * K_ELEMS + buf * V_ELEMS;  // row-major V
-        if (QB >= 2 && MFA_PIPELINE && !skip && !masked) {
+        if constexpr (EXACT) {
+            if (!skip) {
+                if (masked)
+                    block_exact(std::true_type{}, kbuf, vtb, j);
+                else
+                    block_exact(std::false_type{}, kbuf, vtb, j);
+            }
+            stage_next();
+        } else if (QB >= 2 && MFA_PIPELINE && !skip && !masked) {
             if constexpr (QB >= 2 && MFA_PIPELINE) {
                 if constexpr (MFA_STAGE_IN_PV && MFA_BRANCHFREE_STAGE) {
                     // unconditional staging: no branch splits the pipelined
@@ -1103,6 +1218,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
     const SeqView sv = seq_view<2>(a, b, hq);
     const int q0 = tile * BM;
     if (q0 >= sv.Lq) return;
+    if (a.single_rows != 0 && sv.Lq == 1) return;  // (the exact-row kernel's launch computes it)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, half = lane >> 5;
@@ -1549,6 +1665,7 @@ mfa_fwd16_tk_kernel(KArgs a) {
     const SeqView sv = seq_view<2>(a, b, hq);
     const int q0 = tile * BM;
     if (q0 >= sv.Lq) return;
+    if (a.single_rows != 0 && sv.Lq == 1) return;  // (the exact-row kernel's launch computes it)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, half = lane >> 5;
     const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
@@ -1916,13 +2033,24 @@ struct KernelCfg {
     int threads = kThreads;  // threads per workgroup
 };
 
-template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS>
+template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, bool EXACT = false>
 KernelCfg cfg16(const char* name, bool paged) {
     constexpr int BM = kWaves * QB * 32, BN = NKB * 32;
     constexpr int kv = 2 * (BN * (DP + 8) + BN * (DP + MFA_V_PAD)), qs = BM * (DP + 8);
-    return KernelCfg{paged ? (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, true>
-                           : (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, false>,
+    return KernelCfg{paged ? (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, true, EXACT>
+                           : (kernel_fn)mfa_fwd16_kernel<DP, QB, NKB, IS_BF16, BIAS, false, EXACT>,
                      BM, BN, 2 * (kv > qs ? kv : qs), name};
+}
+// the exact-row kernel: one 32-row query block per wavefront (128-row tiles),
+// 64-key blocks
+template <bool IS_BF16, bool BIAS>
+KernelCfg select16x(int dp, bool paged) {
+    switch (dp) {
+        case 32: return cfg16<32, 1, 2, IS_BF16, BIAS, true>(IS_BF16 ? "mfa_fwd16x<bf16,d32>" : "mfa_fwd16x<f16,d32>", paged);
+        case 64: return cfg16<64, 1, 2, IS_BF16, BIAS, true>(IS_BF16 ? "mfa_fwd16x<bf16,d64>" : "mfa_fwd16x<f16,d64>", paged);
+        case 96: return cfg16<96, 1, 2, IS_BF16, BIAS, true>(IS_BF16 ? "mfa_fwd16x<bf16,d96>" : "mfa_fwd16x<f16,d96>", paged);
+        default: return cfg16<128, 1, 2, IS_BF16, BIAS, true>(IS_BF16 ? "mfa_fwd16x<bf16,d128>" : "mfa_fwd16x<f16,d128>", paged);
+    }
 }
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, int NW = 8>
 KernelCfg cfg16pp(const char* name) {
@@ -2031,7 +2159,21 @@ struct Plan {
     bool empty;
     kernel_fn combine = nullptr;  // split-KV merge kernel
     int64_t ws_bytes = 0;         // split-KV workspace
+    // second launch (after the first, before a split-KV merge): the exact-row
+    // kernel on the single-row sequences of a varlen call that mixes them
+    // with longer ones
+    bool second = false;
+    KernelCfg cfg2;
+    KArgs args2;
+    int grid2 = 0;
 };
+
+// Enqueue a plan's kernel launches (the split-KV merge aside).
+void launch_plan(const Plan& plan, hipStream_t st) {
+    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, st, plan.args);
+    if (plan.second)
+        hipLaunchKernelGGL(plan.cfg2.fn, dim3(plan.grid2), dim3(plan.cfg2.threads), 0, st, plan.args2);
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -2146,8 +2288,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     bool pack = false;
     const bool lse_ok = p->cu_seqlens_q ? !p->softmax_lse : (!p->softmax_lse || p->lse_head_stride == 1);
     if (p->dtype_in != MFA_DTYPE_F32 && p->seqlen_q == 1 && p->heads_kv > 0 && p->heads_q > p->heads_kv &&
-        p->heads_q % p->heads_kv == 0 && p->window_left < 0 && p->window_right < 0 && !p->alibi_slopes && lse_ok &&
-        p->tile_hint != MFA_TILE_PINGPONG && p->tile_hint != MFA_TILE_PINGPONG256) {
+        p->heads_q % p->heads_kv == 0 && p->window_left < 0 && p->window_right < 0 && !p->alibi_slopes && lse_ok) {
         const int R = p->heads_q / p->heads_kv;
         packed = *p;
         packed.seqlen_q = R;
@@ -2327,14 +2468,29 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         else
             pp256 = prefer_pp256(p, geom.cus);
     }
+    // Exact rows: a 16-bit call whose every sequence has one query row, or a
+    // packed grouped-query decode, runs the exact-row kernel (two-term
+    // probabilities, per-row rescales), whatever the tile hint.  A varlen
+    // call that may mix single-row sequences with longer ones runs its kernel
+    // on the longer ones and the exact-row kernel on the single-row ones
+    // (a second launch, planned below), so each sequence's rows are those of
+    // its own dense call.
+    const bool exact_call = din != MFA_DTYPE_F32 && (pack || p->seqlen_q == 1);
+    const bool mixed_rows = din != MFA_DTYPE_F32 && !exact_call && p->cu_seqlens_q != nullptr;
     // At most 32 keys per sequence under many query rows (cross-attention to
     // a short conditioning sequence): the tiny-key kernel, which keeps the
     // keys in registers and streams the query rows (measured at bf16 D=128
     // Lq=26136 Lk=5 H=16: see the design notes)
     const bool tiny_keys = MFA_TK && p->tile_hint == MFA_TILE_AUTO && din != MFA_DTYPE_F32 && !paged &&
-                           split_keys == 0 && p->seqlen_k <= 32 && p->seqlen_q >= MFA_TK_MIN_ROWS;
+                           !exact_call && split_keys == 0 && p->seqlen_k <= 32 && p->seqlen_q >= MFA_TK_MIN_ROWS;
+    auto exact_cfg = [&]() {
+        if (din == MFA_DTYPE_BF16) return bias ? select16x<true, true>(dp, paged) : select16x<true, false>(dp, paged);
+        return bias ? select16x<false, true>(dp, paged) : select16x<false, false>(dp, paged);
+    };
     if (din == MFA_DTYPE_F32)
         plan->cfg = bias ? select32<true>(dp, paged) : select32<false>(dp, paged);
+    else if (exact_call)
+        plan->cfg = exact_cfg();
     else if (tiny_keys && din == MFA_DTYPE_BF16)
         plan->cfg = bias ? select16tk<true, true>(dp) : select16tk<true, false>(dp);
     else if (tiny_keys)
@@ -2376,6 +2532,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     a.qts = tok_qs;
     a.ots = tok_os;
     a.pack_r = (pack && p->cu_seqlens_q) ? p->seqlen_q : 1;  // packed varlen: R rows per query token
+    a.single_rows = mixed_rows ? 1 : 0;
     a.out_f32 = dout == MFA_DTYPE_F32 ? 1 : 0;
     a.lse = p->softmax_lse;
     a.lse_b = p->lse_batch_stride;
@@ -2443,6 +2600,17 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         plan->combine = din == MFA_DTYPE_BF16 ? (kernel_fn)mfa_combine_kernel<true> : (kernel_fn)mfa_combine_kernel<false>;
     }
     if (plan->grid == 0) plan->empty = true;
+    plan->second = false;
+    if (mixed_rows && !plan->empty) {
+        // the exact-row kernel over one query tile (times the split chunks)
+        // of every (sequence, head); it computes the single-row sequences only
+        plan->second = true;
+        plan->cfg2 = exact_cfg();
+        plan->args2 = a;
+        plan->args2.single_rows = 2;
+        plan->args2.T = a.nsplit;
+        plan->grid2 = (a.grouped ? X * a.upx : a.U) * plan->args2.T;
+    }
     return MFA_OK;
 }
 
@@ -2477,8 +2645,10 @@ int launch_splitkv(Plan& plan, void* ws, hipStream_t st, const char* who) {
     const int64_t rows = (int64_t)a.nsplit * a.U * a.Lq;
     a.ws_o = static_cast<float*>(ws);
     a.ws_lse = a.ws_o + rows * a.ws_ld;
-    // one chunk (every key range fits): the kernel stores O itself
-    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, st, a);
+    plan.args2.ws_o = a.ws_o;
+    plan.args2.ws_lse = a.ws_lse;
+    // one chunk (every key range fits): the kernels store O themselves
+    launch_plan(plan, st);
     if (a.nsplit > 1)
         hipLaunchKernelGGL(plan.combine, dim3((unsigned)((int64_t)a.U * a.Lq)), dim3(64), 0, st, a);
     const hipError_t e = hipGetLastError();
@@ -2616,7 +2786,7 @@ int mfa_fwd(const mfa_fwd_params* params, void* stream) {
     const int rc = make_plan(params, &plan, chip_geometry_of(static_cast<hipStream_t>(stream)));
     if (rc != MFA_OK) return rc;
     if (plan.empty) return MFA_OK;
-    hipLaunchKernelGGL(plan.cfg.fn, dim3(plan.grid), dim3(plan.cfg.threads), 0, static_cast<hipStream_t>(stream), plan.args);
+    launch_plan(plan, static_cast<hipStream_t>(stream));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(MFA_ERR_LAUNCH, "mfa_fwd: launch failed: %s", hipGetErrorString(e));
     return MFA_OK;

@@ -399,3 +399,29 @@ def test_plan_uses_the_device_geometry():
         pytest.skip("the default leg assumes 256 CUs; a visible device reports its own")
     assert out[None][0].startswith("mfa_fwd16<bf16,d64") and out[None][1] == "2048"
     assert out[32][0].startswith("mfa_fwd16pp<bf16,d64,2,2>") and out[32][1] == "0"
+
+
+def test_exact_row_kernel_choice(lib):
+    # single-row 16-bit calls (one row per head, or packed grouped-query
+    # decode rows) run the exact-row kernel whatever the tile hint; fp32 keeps
+    # its own kernel; longer rows never take it as their main kernel
+    def name(**kw):
+        p = good_params(B=kw.pop("B", 4), L=4096, H=kw.pop("H", 16), Hkv=kw.pop("Hkv", 16), D=kw.pop("D", 128),
+                        dtype=kw.pop("dtype", _hip.MFA_DTYPE_BF16))
+        p.seqlen_q = kw.pop("Lq", 1)
+        for f, val in kw.items():
+            setattr(p, f, val)
+        return _hip.launch_info(p).kernel_name
+    assert name().startswith(b"mfa_fwd16x<bf16,d128>")
+    assert name(Hkv=2).startswith(b"mfa_fwd16x<bf16,d128>")  # packed: 8 rows per K/V head
+    assert name(D=64, dtype=_hip.MFA_DTYPE_F16).startswith(b"mfa_fwd16x<f16,d64>")
+    assert name(D=64, tile_hint=_hip.MFA_TILE_PINGPONG).startswith(b"mfa_fwd16x<bf16,d64>")
+    assert name(softcap=5.0).startswith(b"mfa_fwd16x<bf16,d128>")
+    assert name(dtype=_hip.MFA_DTYPE_F32).startswith(b"mfa_fwd32")
+    assert not name(Lq=2).startswith(b"mfa_fwd16x")
+    assert not name(Lq=4096).startswith(b"mfa_fwd16x")
+    # varlen: one query row per sequence at most -> exact kernel; longer
+    # sequences -> their kernel (the single-row ones get the exact kernel's
+    # second launch)
+    assert name(Lq=1, cu_seqlens_q=256, cu_seqlens_k=256).startswith(b"mfa_fwd16x")
+    assert not name(Lq=64, cu_seqlens_q=256, cu_seqlens_k=256).startswith(b"mfa_fwd16x")

@@ -5,11 +5,12 @@ split-KV chunk choice.  Deterministic (seeded), so it is an ordinary
 regression test with a wide net, not a fuzzer.
 
 Bars: fp32 within 1e-5 of the float64 restatement (oracle/stream_ref.c);
-bf16/fp16 within the north-star bars against the chunked oracle with a 1.25x
-allowance: a random draw lands on near-uniform rows (small or negative
-scales, D = 8, one row over ~10^3 keys), where O averages many values and the
-rounding of each probability to 16 bits before the PV product alone reaches
-~2^-9 of max|ref| (measured up to 1.2x the bars in such draws)."""
+bf16/fp16 within the north-star bars against the chunked oracle, with no
+allowance and no exception: 2e-3*max|ref| on the fp32 output and
+4e-3*max|ref| on the 16-bit output, on every draw.  Draws with one query
+row over many keys, where O averages near-equal weights and one 16-bit
+rounding of each would be visible against the small max|ref|, run the
+exact-row kernel (two-term probabilities)."""
 from __future__ import annotations
 
 import random
@@ -25,7 +26,6 @@ from gpu_util import DEV, FP32_ATOL, REL_16, REL_16_OUT, make_qkv, make_varlen, 
 
 pytestmark = pytest.mark.gpu
 
-ALLOW = 1.25
 CASES = 160
 
 
@@ -109,10 +109,14 @@ def test_random_case(i, monkeypatch):
         assert (out.cpu().double() - exact).abs().max().item() <= FP32_ATOL, what
         return
     ref_max = max(ref.abs().max().item(), 1e-6)
-    assert max_err(out, ref) <= ALLOW * REL_16_OUT * ref_max, what
+    assert max_err(out, ref) <= REL_16_OUT * ref_max, what
+    ws = kw.get("window_size", (-1, -1))
+    scale = kw.get("softmax_scale", D ** -0.5)
     if shape[0] == "dense":
-        ws = kw.get("window_size", (-1, -1))
-        o32 = _kernel.forward_bshd(q, k, v, kw.get("softmax_scale", D ** -0.5), kw.get("causal", False),
-                                   kw.get("softcap", 0.0), ws[0], ws[1], kw.get("alibi_slopes"),
-                                   out_dtype=torch.float32)
-        assert max_err(o32, ref) <= ALLOW * REL_16 * ref_max, what
+        o32 = _kernel.forward_bshd(q, k, v, scale, kw.get("causal", False), kw.get("softcap", 0.0), ws[0], ws[1],
+                                   kw.get("alibi_slopes"), out_dtype=torch.float32)
+    else:
+        o32 = _kernel.forward_varlen(q, k, v, cu_q, cu_k, max(lq + [1]), max(lk + [1]), scale,
+                                     kw.get("causal", False), kw.get("softcap", 0.0), ws[0], ws[1],
+                                     alibi_slopes=kw.get("alibi_slopes"), out_dtype=torch.float32)
+    assert max_err(o32, ref) <= REL_16 * ref_max, what

@@ -134,23 +134,24 @@ def test_reference_trace_shape():
 
 @pytest.mark.parametrize("dtype", DTYPES16)
 @pytest.mark.parametrize("Lk,D", [(5, 128), (32, 64), (1, 96)])
-def test_packed_grouped_query_decode(dtype, Lk, D, hint):
-    # one query row per sequence with 128 query heads per K/V head: the
-    # single-row grouped-query packing gives 128 rows per K/V head, which is
-    # enough query rows for the tiny-key kernel (decode_pack = 1 there)
+def test_packed_grouped_query_decode_with_few_keys(dtype, Lk, D, hint):
+    # one query row per sequence with 128 query heads per K/V head: packed
+    # into 128 rows per K/V head, enough rows for the tiny-key kernel's
+    # threshold, but packed decode rows always run the exact-row kernel
+    # (two-term probabilities), as any single-row call does
     B, Hq, Hkv = 3, 128, 1
     q, k, v = make_qkv(B, 1, Lk, Hq, Hkv, D, dtype, seed=40 + Lk)
-    assert _kernel.launch_info(q, k, v).kernel_name.startswith(b"mfa_fwd16tk")
+    assert _kernel.launch_info(q, k, v).kernel_name.startswith(b"mfa_fwd16x")
     for kw in (dict(), dict(causal=True), dict(softcap=6.0, softmax_scale=0.2)):
         out = mfa.flash_attn_func(q, k, v, **kw)
         out32 = _fp32_out(q, k, v, kw)
         ref = _oracle(q, k, v, kw)
-        assert_parity(out32, ref, dtype, f"packed tiny-key decode fp32 out Lk={Lk} D={D} {kw}")
-        assert_output(out, ref, dtype, f"packed tiny-key decode Lk={Lk} D={D} {kw}")
-        # K/V repeated per query head: no packing, the 4-wavefront kernel
+        assert_parity(out32, ref, dtype, f"packed decode, few keys, fp32 out Lk={Lk} D={D} {kw}")
+        assert_output(out, ref, dtype, f"packed decode, few keys Lk={Lk} D={D} {kw}")
+        # K/V repeated per query head: no packing, each head alone
         rep = mfa.flash_attn_func(q, k.repeat_interleave(Hq, 2), v.repeat_interleave(Hq, 2), **kw)
         assert torch.equal(out, rep), kw
-        # the packed call on the 4-wavefront kernel
+        # a tile hint does not move exact rows off their kernel
         hint(_hip.MFA_TILE_256)
         assert torch.equal(out, mfa.flash_attn_func(q, k, v, **kw)), kw
         hint(_hip.MFA_TILE_AUTO)
@@ -159,8 +160,29 @@ def test_packed_grouped_query_decode(dtype, Lk, D, hint):
     qv, kv_, vv, cu_q, cu_k = make_varlen([1, 1, 1], lens_k, Hq, Hkv, D, dtype, seed=50 + Lk)
     outv = mfa.flash_attn_varlen_func(qv, kv_, vv, cu_q, cu_k, 1, max(lens_k))
     refv = chunked.flash_attn_varlen_func(qv.cpu(), kv_.cpu(), vv.cpu(), cu_q.cpu(), cu_k.cpu())
-    assert_output(outv, refv, dtype, f"packed tiny-key varlen decode Lk={Lk} D={D}")
+    assert_output(outv, refv, dtype, f"packed varlen decode, few keys Lk={Lk} D={D}")
     sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()
     for i in range(3):
         dense = mfa.flash_attn_func(qv[None, i:i + 1], kv_[None, sk[i]:sk[i + 1]], vv[None, sk[i]:sk[i + 1]])[0]
         assert torch.equal(outv[i:i + 1], dense), i
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+def test_single_row_sequences_among_many_rows(dtype):
+    # a varlen batch on the tiny-key kernel that also holds single-row
+    # sequences: those run the exact-row kernel's launch, so every sequence
+    # equals its dense call bit for bit
+    lens_q, lens_k = [300, 1, 513, 1, 0], [5, 9, 32, 30, 4]
+    q, k, v, cu_q, cu_k = make_varlen(lens_q, lens_k, 4, 2, 64, dtype, seed=60)
+    for kw in (dict(), dict(causal=True), dict(softcap=3.0)):
+        out = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens_q), max(lens_k), **kw)
+        sq = [0] + torch.tensor(lens_q).cumsum(0).tolist()
+        sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()
+        for i in range(len(lens_q)):
+            if lens_q[i] == 0:
+                continue
+            dense = mfa.flash_attn_func(q[None, sq[i]:sq[i + 1]], k[None, sk[i]:sk[i + 1]], v[None, sk[i]:sk[i + 1]],
+                                        **kw)[0]
+            assert torch.equal(out[sq[i]:sq[i + 1]], dense), (kw, i)
+        ref = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), **kw)
+        assert_output(out, ref, dtype, f"mixed varlen {kw}")
