@@ -797,6 +797,18 @@ mfa_fwd16_kernel(KArgs a) {
     // valid key row: rows past the sequence read as zero in hardware, and a
     // chunk past the head dim gets an offset beyond the resource (zero too),
     // so the loads carry no per-chunk conditions and no 64-bit address math.
+    // At head dims 32 and 64 the threads cover whole rows: a lane's chunks
+    // i = 0..KCH-1 share one column and sit RSTEP rows apart, so only chunk
+    // 0's offsets are kept and the others are formed in the loop from
+    // uniform row steps (the registers of KCH-1 offsets per operand are free
+    // for the rest of the kernel: without them the D = 64 two-block tile
+    // spilled 16-20 bytes, with a reload inside the loop).  A lane past the
+    // head dim keeps an offset >= 2^31 for every chunk (the row steps stay
+    // below 2^31: the planner bounds 63 rows of a stride to 2 GiB), so it
+    // still reads zeros.  Not at head dim 128, which does not spill and whose
+    // VALU-bound biased tiles measured 1 % slower with the in-loop adds.
+    constexpr bool kRowStep = DP <= 64 && (kThreads % CPR == 0) && (KCH * kThreads == BN * CPR);
+    constexpr int RSTEP = kThreads / CPR;
     u32x4_t kreg[KCH], vreg[KCH];
     uint32_t koff[KCH], voff[KCH];
     int lds_off[KCH], vlds_off[KCH];
@@ -810,6 +822,7 @@ mfa_fwd16_kernel(KArgs a) {
         lds_off[i] = (cc < BN * CPR) ? row * KST + col : -1;
         vlds_off[i] = (cc < BN * CPR) ? row * VST + col : -1;
     }
+    const uint32_t kstep = (uint32_t)(RSTEP * a.ks * 2), vstep = (uint32_t)(RSTEP * a.vs * 2);
     auto gload = [&](int j0) {
         // rows <= 0 (a block past the sequence, loaded branch-free by the
         // pipelined path) or a block before jbeg (past a reversed walk) gives
@@ -832,10 +845,23 @@ mfa_fwd16_kernel(KArgs a) {
             (void*)(sv.k + kbo * 2), (short)0, kbytes, kBufferDword3);
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(sv.v + vbo * 2), (short)0, vbytes, kBufferDword3);
+        if constexpr (kRowStep && KCH > 1) {
+            // (pinned copies: the per-chunk offsets are formed here, in the
+            // loop, not hoisted out of it as KCH live registers)
+            uint32_t k0 = koff[0], v0 = voff[0];
+            pin(k0);
+            pin(v0);
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
-            vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0);
+            for (int i = 0; i < KCH; ++i) {
+                kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, k0 + i * kstep, 0, 0);
+                vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, v0 + i * vstep, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < KCH; ++i) {
+                kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0);
+                vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0);
+            }
         }
     };
     auto swrite = [&](int buf) {
@@ -843,9 +869,13 @@ mfa_fwd16_kernel(KArgs a) {
         uint16_t* vbuf = smem + 2 * K_ELEMS + buf * V_ELEMS;
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
+            // (whole rows: chunk i is RSTEP rows below chunk 0, a constant
+            // LDS offset)
+            const int ko = kRowStep ? lds_off[0] + i * RSTEP * KST : lds_off[i];
+            const int vo = kRowStep ? vlds_off[0] + i * RSTEP * VST : vlds_off[i];
             if (KCH * kThreads == BN * CPR || lds_off[i] >= 0) {
-                *reinterpret_cast<u32x4_t*>(kbuf + lds_off[i]) = kreg[i];
-                *reinterpret_cast<u32x4_t*>(vbuf + vlds_off[i]) = vreg[i];
+                *reinterpret_cast<u32x4_t*>(kbuf + ko) = kreg[i];
+                *reinterpret_cast<u32x4_t*>(vbuf + vo) = vreg[i];
             }
         }
     };

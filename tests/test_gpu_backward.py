@@ -285,3 +285,85 @@ def test_long_rows_config3_shape():
         errs = [rel_err(a, b) for a, b in zip(got, ref)]
         print(f"config3 shape head {h}: dq {errs[0]:.2e} dk {errs[1]:.2e} dv {errs[2]:.2e} (x max|ref|)")
         check_grads(got, ref, torch.float16, f"config3 shape head {h}")
+
+
+def test_long_rows_config2_shape():
+    """Gradients at config 2's shape (bf16, B=1, L=8192, H=16, D=64,
+    non-causal; inputs from seed 1): the full dq/dk/dv of heads 0 and 15
+    against the oracle's autograd."""
+    q, k, v = make_qkv(1, 8192, 8192, 16, 16, 64, torch.bfloat16, seed=1)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(4)).to(DEV, torch.bfloat16)
+    dq, dk, dv = fp32_grads(q, k, v, dout, default_scale(64))
+    torch.cuda.synchronize()
+    for h in (0, 15):
+        sl = slice(h, h + 1)
+        ref = chunked.attention_grads(q[:, :, sl], k[:, :, sl], v[:, :, sl], dout[:, :, sl])
+        got = (dq[:, :, sl], dk[:, :, sl], dv[:, :, sl])
+        errs = [rel_err(a, b) for a, b in zip(got, ref)]
+        print(f"config2 shape head {h}: dq {errs[0]:.2e} dk {errs[1]:.2e} dv {errs[2]:.2e} (x max|ref|)")
+        check_grads(got, ref, torch.bfloat16, f"config2 shape head {h}")
+
+
+def test_config4_shape_varlen_gqa():
+    """Gradients at config 4's shape (bf16 varlen, lengths from seed 3, Hq=32,
+    Hkv=8, D=128, causal): every sequence and head runs on the kernels (dK/dV
+    of a K/V head summed over its 4 query heads from fp32 partials); the
+    oracle checks K/V head groups 0 and 7 (query heads 0-3 and 28-31) of the
+    longest (3501) and the shortest (863) sequence in full."""
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(256, 4097, (8,), generator=g)
+    T = int(lens.sum())
+    q = torch.randn(T, 32, 128, generator=g).to(DEV, torch.bfloat16)
+    k = torch.randn(T, 8, 128, generator=g).to(DEV, torch.bfloat16)
+    v = torch.randn(T, 8, 128, generator=g).to(DEV, torch.bfloat16)
+    cu = torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)]).to(torch.int32).to(DEV)
+    mx = int(lens.max())
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(5)).to(DEV, torch.bfloat16)
+    out, lse = _kernel.forward_varlen(q, k, v, cu, cu, mx, mx, default_scale(128), True, return_lse=True)
+    dq, dk, dv = _kernel._run_bwd(q[None], k[None], v[None], out[None], dout[None], lse, scale=default_scale(128),
+                                  causal=True, softcap=0.0, window_left=-1, window_right=-1, alibi=None,
+                                  alibi_bstride=0, cu_q=cu, cu_k=cu, seqlen_q=mx, seqlen_k=mx, grad_f32=True)
+    torch.cuda.synchronize()
+    starts = [0] + lens.cumsum(0).tolist()
+    ls = lens.tolist()
+    for i in (ls.index(max(ls)), ls.index(min(ls))):
+        a, b = starts[i], starts[i + 1]
+        for grp in (0, 7):
+            hq, hk = slice(4 * grp, 4 * grp + 4), slice(grp, grp + 1)
+            ref = chunked.attention_grads(q[None, a:b, hq], k[None, a:b, hk], v[None, a:b, hk], dout[None, a:b, hq],
+                                          causal=True)
+            got = (dq[:, a:b, hq], dk[:, a:b, hk], dv[:, a:b, hk])
+            errs = [rel_err(x, y) for x, y in zip(got, ref)]
+            print(f"config4 shape seq {i} (L={b - a}) kv head {grp}: dq {errs[0]:.2e} dk {errs[1]:.2e} "
+                  f"dv {errs[2]:.2e} (x max|ref|)")
+            check_grads(got, ref, torch.bfloat16, f"config4 shape seq {i} kv head {grp}")
+
+
+def test_config5_shape_window_softcap_alibi():
+    """Gradients at config 5's shape (bf16, B=1, L=32768, H=16, D=128, causal,
+    window (2048, 0), soft-cap 30, ALiBi 2^(-8(i+1)/16), inputs N(0,1)*0.5
+    from seed 4): every head runs on the kernels.  The oracle runs on slices
+    of heads 0 and 15: rows [a, a+4096) against keys [a-2048, a+4096) keep
+    every position difference i - j (bottom-right causal, window and ALiBi
+    distances) of the full problem, so dq of those rows and dk/dv of keys
+    [a, a+2048) -- whose every contributing row lies in the slice -- are
+    exact; a = 0 (before the window fills) and a = 16384."""
+    L, H, D = 32768, 16, 128
+    q, k, v = make_qkv(1, L, L, H, H, D, torch.bfloat16, seed=4, scale_inputs=0.5)
+    slopes = torch.tensor([2 ** (-8 * (i + 1) / 16) for i in range(H)], dtype=torch.float32, device=DEV)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(6)).to(DEV, torch.bfloat16)
+    kw = dict(causal=True, softcap=30.0, wl=2048, wr=0, alibi=slopes)
+    dq, dk, dv = fp32_grads(q, k, v, dout, default_scale(D), **kw)
+    torch.cuda.synchronize()
+    for a in (0, 16384):
+        k0 = max(a - 2048, 0)
+        for h in (0, 15):
+            sl = slice(h, h + 1)
+            ref = chunked.attention_grads(q[:, a:a + 4096, sl], k[:, k0:a + 4096, sl], v[:, k0:a + 4096, sl],
+                                          dout[:, a:a + 4096, sl], causal=True, window_size=(2048, 0), softcap=30.0,
+                                          alibi_slopes=slopes[sl].cpu())
+            got = (dq[:, a:a + 4096, sl], dk[:, a:a + 2048, sl], dv[:, a:a + 2048, sl])
+            ref = (ref[0], ref[1][:, a - k0:a - k0 + 2048], ref[2][:, a - k0:a - k0 + 2048])
+            errs = [rel_err(x, y) for x, y in zip(got, ref)]
+            print(f"config5 shape rows {a}.. head {h}: dq {errs[0]:.2e} dk {errs[1]:.2e} dv {errs[2]:.2e} (x max|ref|)")
+            check_grads(got, ref, torch.bfloat16, f"config5 shape rows {a} head {h}")
