@@ -62,6 +62,13 @@ struct KArgs {
     // (the exact-row kernel's launch computes them), 2 = this launch (the
     // exact-row kernel) computes only them
     int32_t single_rows;
+    // ping-pong tiles packing the query heads of one K/V head (grouped-query
+    // calls): hpack heads share a tile and its K/V stream, each taking
+    // 1/hpack of the tile's rows at the same positions.  The unit heads Hq
+    // are then groups of hpack heads (qh / oh / lse_h step a whole group) and
+    // qh1 / oh1 / lse_h1 step one head inside it.  hpack = 1: one head.
+    int32_t hpack;
+    int64_t qh1, oh1, lse_h1;
     int32_t out_f32;
     // schedule
     int32_t T;        // query tiles per (sequence, head)

@@ -1246,7 +1246,13 @@ mfa_fwd16_pp_kernel(KArgs a) {
     int b, hq, tile;
     if (!decode_tile(a, blockIdx.x, b, hq, tile)) return;
     const SeqView sv = seq_view<2>(a, b, hq);
-    const int q0 = tile * BM;
+    // Head-packed tiles (a.hpack > 1): the tile holds PM positions of each of
+    // hpack query heads of one K/V head, head-major (tile row = head * PM +
+    // position), so wave w takes head w / (NW / hpack) at position block
+    // w % (NW / hpack) and every wave reads its rows at LDS row w * QB * 32.
+    const int hpk = a.hpack;
+    const int PM = BM / hpk;  // positions per tile
+    const int q0 = tile * PM;
     if (q0 >= sv.Lq) return;
     if (a.single_rows != 0 && sv.Lq == 1) return;  // (the exact-row kernel's launch computes it)
 
@@ -1254,18 +1260,21 @@ mfa_fwd16_pp_kernel(KArgs a) {
     const int l32 = lane & 31, half = lane >> 5;
     const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
     const int dq = Lk - Lq;
+    const int wph = NW / hpk;                  // waves per head
+    const int hl = wave / wph;                 // this wave's head inside the tile
+    const int wq0 = q0 + (wave - hl * wph) * QB * 32;  // first position of this wavefront
 
     // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
     if (tid < 4) simd_count[tid] = 0;
     for (int c = tid; c < BM * CPR; c += NT) {
         const int row = c / CPR, col = (c % CPR) * 8;
+        const int h = row / PM, pos = q0 + row - h * PM;
         u32x4_t val = {0, 0, 0, 0};
-        if (q0 + row < Lq && col < D)
-            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 2);
+        if (pos < Lq && col < D)
+            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)h * a.qh1 + (int64_t)pos * a.qs + col) * 2);
         *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
     }
     __syncthreads();
-    const int wq0 = q0 + wave * QB * 32;
     op_t qf[QB][DS];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
@@ -1286,7 +1295,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
         rs[qb].center = wq0 + 32 * qb + l32 + dq;
         rs[qb].lo = key_lo(a, rs[qb].center);
         rs[qb].hi = key_hi(a, rs[qb].center, Lk);
-        rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+        rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq * hpk + hl] : 0.f;
         row_reset(rs[qb]);
         const int r0 = wq0 + 32 * qb;
         const int r1 = max(min(r0 + 31, Lq - 1), r0);
@@ -1306,14 +1315,19 @@ mfa_fwd16_pp_kernel(KArgs a) {
     const float tau = Lq == 1 ? 0.f : (float)MFA_RESCALE_TAU;
     const float tau_c = tau / c;
 
+    // this wave's head: its O and lse rows
+    SeqView svh = sv;
+    svh.o += (int64_t)hl * a.oh1 * (a.out_f32 ? 4 : 2);
+    if (svh.lse) svh.lse += (int64_t)hl * a.lse_h1;
+
     // ---- key range of the workgroup
-    const int qlast = min(q0 + BM, Lq) - 1;
+    const int qlast = min(q0 + PM, Lq) - 1;
     const int klo = key_lo(a, q0 + dq);
     const int khi = key_hi(a, qlast + dq, Lk);
     const int jbeg = (klo / BN) * BN;
     const int nblk = khi >= klo ? (khi - jbeg) / BN + 1 : 0;
     if (nblk == 0) {  // no valid key for any row of the tile: zeros
-        store_out<QB, DB, IS_BF16>(a, sv, o, rs, wq0, lane, c);
+        store_out<QB, DB, IS_BF16>(a, svh, o, rs, wq0, lane, c);
         return;
     }
     // key block of step u, last block first under ALiBi (as in the
@@ -1645,7 +1659,7 @@ mfa_fwd16_pp_kernel(KArgs a) {
     // nor in the O blocks below (every wavefront's loads done, then a barrier)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    store_out_rows<QB, DB, IS_BF16, KST>(a, sv, o, rs, wq0, lane, c, smem + wave * QB * 32 * KST);
+    store_out_rows<QB, DB, IS_BF16, KST>(a, svh, o, rs, wq0, lane, c, smem + wave * QB * 32 * KST);
 }
 
 // ----------------------------------------------------------------------------
@@ -2137,6 +2151,10 @@ KernelCfg cfg32(const char* name, bool paged) {
 #ifndef MFA_PINGPONG
 #define MFA_PINGPONG 1
 #endif
+// ping-pong tiles pack the query heads of a K/V head (2, 4 or 8 of them)
+#ifndef MFA_PP_HEAD_PACK
+#define MFA_PP_HEAD_PACK 1
+#endif
 // paged K/V (block_table) runs on the 256-row and fp32 kernels only
 template <bool IS_BF16, bool BIAS>
 KernelCfg select16(int dp, bool fills_chip, bool paged, bool pp256) {
@@ -2589,12 +2607,32 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         a.bt_b = 0;
     }
 
-    const int rows = plan->cfg.rows;
+    // Ping-pong tiles of a grouped-query call with 2, 4 or 8 query heads per
+    // K/V head pack those heads into one tile (KArgs.hpack): each head takes
+    // 1/R of the tile's rows at the same positions, so a tile streams its K/V
+    // once for R heads, and a causal tile spans 1/R of the positions (fewer
+    // partly masked diagonal blocks).  Rows of one wavefront are still 32
+    // consecutive positions of one head aligned to 32, so every row's
+    // arithmetic equals the unpacked call's (grouped-query heads equal
+    // repeated K/V heads bit for bit).
+    a.hpack = 1;
+    a.qh1 = a.qh;
+    a.oh1 = a.oh;
+    a.lse_h1 = a.lse_h;
+    const int R = p->heads_q / p->heads_kv;
+    if (MFA_PP_HEAD_PACK && plan->cfg.threads == 8 * 64 && (R == 2 || R == 4 || R == 8)) {
+        a.hpack = R;
+        a.Hq = p->heads_kv;
+        a.qh = p->q_head_stride * R;
+        a.oh = p->o_head_stride * R;
+        a.lse_h = p->lse_head_stride * R;
+    }
+    const int rows = plan->cfg.rows / a.hpack;  // positions per tile
     a.T = (p->seqlen_q + rows - 1) / rows;
     // (bounded before the int32 product below is formed)
     if ((int64_t)p->batch * p->heads_q * a.T > 0x7fffffffLL / 2)
         return set_err(MFA_ERR_INVALID, "mfa_fwd: problem too large");
-    a.U = p->batch * p->heads_q;
+    a.U = p->batch * a.Hq;
     const int64_t G = (int64_t)p->batch * p->heads_kv;
     const int X = geom.xcds;
     int xshift = 0;
@@ -2603,7 +2641,7 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         a.grouped = 1;
         a.xcd_shift = xshift;
         a.tile_major = (p->causal || p->window_left >= 0 || p->window_right >= 0) ? 1 : 0;
-        a.upx = (int32_t)(G / X) * (p->heads_q / p->heads_kv);
+        a.upx = (int32_t)(G / X) * (a.Hq / p->heads_kv);
         plan->grid = X * a.upx * a.T;
     } else {
         a.grouped = 0;
@@ -2636,10 +2674,19 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         // of every (sequence, head); it computes the single-row sequences only
         plan->second = true;
         plan->cfg2 = exact_cfg();
-        plan->args2 = a;
-        plan->args2.single_rows = 2;
-        plan->args2.T = a.nsplit;
-        plan->grid2 = (a.grouped ? X * a.upx : a.U) * plan->args2.T;
+        KArgs& a2 = plan->args2;
+        a2 = a;
+        a2.single_rows = 2;
+        // (one head per unit: undo a head-packed main launch's strides)
+        a2.hpack = 1;
+        a2.Hq = p->heads_q;
+        a2.qh = a.qh1;
+        a2.oh = a.oh1;
+        a2.lse_h = a.lse_h1;
+        a2.U = p->batch * p->heads_q;
+        a2.upx = a.grouped ? (int32_t)(G / X) * R : 0;
+        a2.T = a.nsplit;
+        plan->grid2 = (a.grouped ? X * a2.upx : a2.U) * a2.T;
     }
     return MFA_OK;
 }
