@@ -54,6 +54,11 @@ namespace {
 #ifndef MFA_BWD_QSB_NARROW
 #define MFA_BWD_QSB_NARROW 2
 #endif
+// dK/dV above head dim 64 on the eight-wavefront kernel (K/V in LDS, two
+// wavefronts per SIMD) instead of the four-wavefront one
+#ifndef MFA_BWD_DKDV8
+#define MFA_BWD_DKDV8 1
+#endif
 // 32-key blocks per dQ step (four: measured 17 % slower at D=128)
 #ifndef MFA_BWD_DQ_NKB
 #define MFA_BWD_DQ_NKB 2
@@ -533,6 +538,265 @@ mfa_bwd_dkdv_kernel(BArgs a) {
     }
 }
 
+// ----------------------------------------------------------------------------
+// dK / dV above head dim 64 on eight wavefronts (two per SIMD): workgroup =
+// 128 keys of one (sequence, K/V head).  Wavefronts w and w+4 own the same 32
+// keys and take the two 32-row sub-blocks of each 64-row query step, so each
+// wavefront computes S, dP, dV and dK for one sub-block per step.  K and V
+// sit in LDS (read as MFMA B operands like the Q / dO rows), which leaves
+// room for two wavefronts per SIMD: while one waits on a barrier, staging or
+// an LDS read, the other's MFMAs run.  Each wavefront of the pair holds a
+// partial dK / dV over its sub-blocks; the pair's sums are added in a fixed
+// order (w + (w+4)) through LDS at the end, so the result does not depend
+// on scheduling.  dP starts from -Dsum (staged negated), so dS = P * dP.
+constexpr int kB8Threads = 512;  // 8 wavefronts
+template <int DP, bool IS_BF16, bool BIAS>
+__global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
+    typedef Ops<IS_BF16> O;
+    typedef typename O::op_t op_t;
+    constexpr int DS = DP / 16, DB = DP / 32;
+    constexpr int NT = kB8Threads;
+    constexpr int BQ = 64;       // query rows per step (two sub-blocks)
+    constexpr int ST = DP + 8;   // LDS row stride (elements) of every tile
+    constexpr int CPR = DP / 8;  // 16-byte chunks per row
+    constexpr int SCH = (BQ * CPR + NT - 1) / NT;   // staged chunks per thread and tensor
+    constexpr int KCH = (128 * CPR + NT - 1) / NT;  // K (and V) chunks per thread
+    // K rows [0, 128) then V rows; reused for the pair sums at the end
+    __shared__ __attribute__((aligned(16))) uint16_t kv_s[2 * 128 * ST];
+    static_assert(sizeof(kv_s) >= 4 * DB * 16 * 64 * sizeof(float), "pair-sum buffer");
+    __shared__ __attribute__((aligned(16))) uint16_t q_s[2][BQ * ST];
+    __shared__ __attribute__((aligned(16))) uint16_t do_s[2][BQ * ST];
+    __shared__ __attribute__((aligned(16))) float lse_s[2][BQ];
+    __shared__ __attribute__((aligned(16))) float ds_s[2][BQ];
+
+    const KArgs& f = a.f;
+    const int bid = blockIdx.x;
+    const int ktile = bid / (a.Ukv * a.G), rem = bid - ktile * (a.Ukv * a.G);
+    const int unit = rem / a.G, grp = rem - unit * a.G;
+    const int b = unit / f.Hkv, hkv = unit - b * f.Hkv;
+    const KView kv = k_view(a, b, hkv);
+    const int Lk = kv.Lk, D = f.D;
+    const int k0 = ktile * 128;
+    if (k0 >= Lk) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kw = wave & 3, sb = wave >> 2;  // key block, query sub-block of each step
+    const int l32 = lane & 31, half = lane >> 5;
+    const int key = k0 + kw * 32 + l32;  // this lane's key (B-operand / accumulator column)
+    const int k1 = min(k0 + 128, Lk) - 1;
+
+    // K and V rows of the workgroup into LDS (rows past the sequence and
+    // columns past the head dim as zeros)
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        const int cc = tid + NT * i;
+        if (KCH * NT == 128 * CPR || cc < 128 * CPR) {
+            const int row = cc / CPR, col = (cc % CPR) * 8;
+            u32x4_t kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+            if (k0 + row < Lk && col < D) {
+                kk = *reinterpret_cast<const u32x4_t*>(kv.k + ((int64_t)(k0 + row) * f.ks + col) * 2);
+                vv = *reinterpret_cast<const u32x4_t*>(kv.v + ((int64_t)(k0 + row) * f.vs + col) * 2);
+            }
+            *reinterpret_cast<u32x4_t*>(kv_s + row * ST + col) = kk;
+            *reinterpret_cast<u32x4_t*>(kv_s + (128 + row) * ST + col) = vv;
+        }
+    }
+    f32x16_t dka[DB], dva[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dka[db][r] = dva[db][r] = 0.f;
+    const float c = BIAS ? kLog2e : f.scale_log2;
+
+    // query blocks: as in mfa_bwd_dkdv_kernel, in 64-row steps
+    const int R = f.Hq / f.Hkv / a.G;
+    const int hq0 = hkv * R * a.G + grp * R;
+    const int Lq = f.cu_q ? f.cu_q[b + 1] - f.cu_q[b] : f.Lq;
+    const int dq = Lk - Lq;
+    int qlo = 0, qhi = Lq - 1;
+    if (f.causal) qlo = max(qlo, k0 - dq);
+    if (f.wr >= 0) qlo = max(qlo, k0 - f.wr - dq);
+    if (f.wl >= 0) qhi = min(qhi, k1 + f.wl - dq);
+    const int qb0 = (qlo / BQ) * BQ;
+    const int nqb = qhi >= qb0 ? (qhi - qb0) / BQ + 1 : 0;
+    const int nsteps = R * nqb;
+
+    // buffer-load staging of Q / dO (rows past the sequence read zero)
+    u32x4_t sq[SCH], sd[SCH];
+    uint32_t qoff[SCH], dooff[SCH];
+    int soff[SCH];
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+        const int cc = tid + NT * i;
+        const int row = cc / CPR, col = (cc % CPR) * 8;
+        const bool in = cc < BQ * CPR && col < D;
+        qoff[i] = in ? (uint32_t)(((int64_t)row * f.qs + col) * 2) : 0x80000000u;
+        dooff[i] = in ? (uint32_t)(((int64_t)row * a.dos + col) * 2) : 0x80000000u;
+        soff[i] = row * ST + col;
+    }
+    float lreg = INFINITY, dreg = 0.f;
+    auto gload = [&](int step) {
+        const int rr = step / nqb;
+        const int q0 = qb0 + (step - rr * nqb) * BQ;
+        const QView qv = q_view(a, b, hq0 + rr);
+        const int rm1 = min(Lq - q0, BQ) - 1;  // q0 < Lq
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(qv.q + (int64_t)q0 * f.qs * 2), (short)0, (int)(((int64_t)rm1 * f.qs + D) * 2), kBufferDword3);
+        const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(qv.dout + (int64_t)q0 * a.dos * 2), (short)0, (int)(((int64_t)rm1 * a.dos + D) * 2), kBufferDword3);
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) {
+            sq[i] = __builtin_amdgcn_raw_buffer_load_b128(qr, qoff[i], 0, 0);
+            sd[i] = __builtin_amdgcn_raw_buffer_load_b128(dr, dooff[i], 0, 0);
+        }
+        if (tid < BQ) {
+            const bool in = q0 + tid < Lq;
+            lreg = in ? lse2_of(qv.lse[q0 + tid]) : INFINITY;
+            dreg = in ? -qv.dsum[q0 + tid] : 0.f;
+        }
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) {
+            if (SCH * NT == BQ * CPR || tid + NT * i < BQ * CPR) {
+                *reinterpret_cast<u32x4_t*>(q_s[buf] + soff[i]) = sq[i];
+                *reinterpret_cast<u32x4_t*>(do_s[buf] + soff[i]) = sd[i];
+            }
+        }
+        if (tid < BQ) {
+            lse_s[buf][tid] = lreg;
+            ds_s[buf][tid] = dreg;
+        }
+    };
+    if (nsteps > 0) {
+        gload(0);
+        swrite(0);
+    }
+    __syncthreads();
+    const uint16_t* kbase = kv_s + (32 * kw + l32) * ST + 8 * half;  // this lane's K row
+    const uint16_t* vbase = kbase + 128 * ST;                         // and V row
+    const int wk0 = k0 + kw * 32;
+    for (int step = 0; step < nsteps; ++step) {
+        const int buf = step & 1;
+        if (step + 1 < nsteps) gload(step + 1);  // in flight during this step's MFMAs
+        const int rr = step / nqb;
+        const int qs0 = qb0 + (step - rr * nqb) * BQ + 32 * sb;  // this wavefront's first query row
+        const int hq = hq0 + rr;
+        const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
+        const uint16_t* qsb = q_s[buf];
+        const uint16_t* dosb = do_s[buf];
+        const float* lsb = lse_s[buf] + 32 * sb;
+        const float* dsb = ds_s[buf] + 32 * sb;
+
+        // S = Q K^T and dP = dO V^T - Dsum (lane = key, registers = query rows)
+        f32x16_t sacc, dpacc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 d4 = *reinterpret_cast<const float4*>(dsb + 8 * g + 4 * half);
+            dpacc[4 * g] = d4.x;
+            dpacc[4 * g + 1] = d4.y;
+            dpacc[4 * g + 2] = d4.z;
+            dpacc[4 * g + 3] = d4.w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sacc[4 * g + i] = 0.f;
+        }
+        const int row = 32 * sb + l32;
+#pragma unroll
+        for (int s = 0; s < DS; ++s) {
+            const op_t qa = *reinterpret_cast<const op_t*>(qsb + row * ST + 16 * s + 8 * half);
+            const op_t kf = *reinterpret_cast<const op_t*>(kbase + 16 * s);
+            const op_t da = *reinterpret_cast<const op_t*>(dosb + row * ST + 16 * s + 8 * half);
+            const op_t vf = *reinterpret_cast<const op_t*>(vbase + 16 * s);
+            sacc = O::mfma(qa, kf, sacc);
+            dpacc = O::mfma(da, vf, dpacc);
+        }
+        // P and dS rounded to 16 bits (register r is query qs0 + acc_row(r) +
+        // 4*half); sub-blocks whose 32 x 32 pairs are all valid skip the masks
+        uint32_t pw[8], dw[8];
+        const bool full = qs0 + 32 <= Lq && key_lo(f, qs0 + 31 + dq) <= wk0 && key_hi(f, qs0 + dq, Lk) >= wk0 + 31;
+        auto probs = [&](auto masked_tag) {
+            constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 l4 = *reinterpret_cast<const float4*>(lsb + 8 * g + 4 * half);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                float p[4], ds[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * g + i;
+                    const int q = qs0 + acc_row(r) + 4 * half;
+                    const int center = q + dq;
+                    float dcap;
+                    const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
+                    const float pe = fast_exp2(fmaf(x, c, -lv[i]));
+                    bool ok = true;
+                    if constexpr (MASKED)
+                        ok = (key <= key_hi(f, center, Lk)) & (key >= key_lo(f, center)) & (q < Lq);
+                    p[i] = ok ? pe : 0.f;
+                    ds[i] = p[i] * dpacc[r];
+                    if constexpr (BIAS) ds[i] *= dcap;
+                }
+                pw[2 * g] = O::pack(p[0], p[1]);
+                pw[2 * g + 1] = O::pack(p[2], p[3]);
+                dw[2 * g] = O::pack(ds[0], ds[1]);
+                dw[2 * g + 1] = O::pack(ds[2], ds[3]);
+            }
+        };
+        if (full)
+            probs(std::false_type{});
+        else
+            probs(std::true_type{});
+        // dV^T += dO^T P, dK^T += Q^T dS (k-slots = query rows of accumulator
+        // registers 8*st..8*st+7)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
+            const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const op_t dot = O::load_tr(dosb, ST, 32 * sb + 16 * st, 32 * db, lane);
+                const op_t qt = O::load_tr(qsb, ST, 32 * sb + 16 * st, 32 * db, lane);
+                dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
+                dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
+            }
+        }
+        if (step + 1 < nsteps) swrite(buf ^ 1);  // the other stage was last read before the previous barrier
+        __syncthreads();
+    }
+    // pair sums: wavefront w + 4 hands its partials to wavefront w through
+    // LDS (every wavefront has passed the last barrier, so K/V are dead)
+    float* red = reinterpret_cast<float*>(kv_s) + kw * (DB * 16 * 64) + lane;
+    auto pair_sum = [&](f32x16_t(&acc)[DB]) __attribute__((always_inline)) {
+        if (sb == 1) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[(db * 16 + r) * 64] = acc[db][r];
+        }
+        __syncthreads();
+        if (sb == 0) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[db][r] += red[(db * 16 + r) * 64];
+        }
+        __syncthreads();
+    };
+    pair_sum(dka);
+    pair_sum(dva);
+    if (sb == 0 && key < Lk) {
+        if (a.G > 1) {  // this group's partial sums, unscaled, fp32
+            const int64_t orow = ((int64_t)grp * a.Ukv + unit) * f.Lk + key;
+            store_rows<DB>(reinterpret_cast<char*>(a.ws_dk + orow * a.ws_ld), 0, D, true, IS_BF16, dka, 1.f, half);
+            store_rows<DB>(reinterpret_cast<char*>(a.ws_dv + orow * a.ws_ld), 0, D, true, IS_BF16, dva, 1.f, half);
+        } else {
+            const bool f32o = a.grad_f32 != 0;
+            const int ges = f32o ? 4 : 2;
+            store_rows<DB>(kv.dk + (int64_t)key * a.dks * ges, 0, D, f32o, IS_BF16, dka, f.scale, half);
+            store_rows<DB>(kv.dv + (int64_t)key * a.dvs * ges, 0, D, f32o, IS_BF16, dva, 1.f, half);
+        }
+    }
+}
+
 // Sum of the G head-group partials of dK / dV in group order (deterministic),
 // scaled (dK) and stored in the gradient dtype: 4 elements per thread.
 template <bool IS_BF16>
@@ -773,6 +1037,7 @@ typedef void (*bkernel_fn)(BArgs);
 
 struct BwdKernels {
     bkernel_fn dsum, dkdv, dq, dkdv_sum;
+    int dkdv_threads;
 };
 
 template <int DP, bool IS_BF16>
@@ -780,7 +1045,15 @@ BwdKernels bwd_kernels(bool bias) {
     BwdKernels k;
     k.dsum = mfa_bwd_dsum_kernel<IS_BF16>;
     k.dkdv_sum = mfa_bwd_dkdv_sum_kernel<IS_BF16>;
-    k.dkdv = bias ? (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, true> : (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, false>;
+    if constexpr (DP > 64 && MFA_BWD_DKDV8) {
+        k.dkdv = bias ? (bkernel_fn)mfa_bwd_dkdv8_kernel<DP, IS_BF16, true>
+                      : (bkernel_fn)mfa_bwd_dkdv8_kernel<DP, IS_BF16, false>;
+        k.dkdv_threads = kB8Threads;
+    } else {
+        k.dkdv = bias ? (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, true>
+                      : (bkernel_fn)mfa_bwd_dkdv_kernel<DP, IS_BF16, false>;
+        k.dkdv_threads = kBThreads;
+    }
     k.dq = bias ? (bkernel_fn)mfa_bwd_dq_kernel<DP, IS_BF16, true> : (bkernel_fn)mfa_bwd_dq_kernel<DP, IS_BF16, false>;
     return k;
 }
@@ -973,7 +1246,7 @@ int mfa_bwd(const mfa_bwd_params* params, void* workspace, int64_t workspace_byt
     a.T = (params->fwd.seqlen_q + 15) / 16;
     hipLaunchKernelGGL(plan.k.dsum, dim3(plan.grid_dsum), dim3(kBThreads), 0, st, a);
     a.T = (params->fwd.seqlen_k + 127) / 128;
-    hipLaunchKernelGGL(plan.k.dkdv, dim3(plan.grid_dkdv), dim3(kBThreads), 0, st, a);
+    hipLaunchKernelGGL(plan.k.dkdv, dim3(plan.grid_dkdv), dim3(plan.k.dkdv_threads), 0, st, a);
     if (a.G > 1) hipLaunchKernelGGL(plan.k.dkdv_sum, dim3(plan.grid_dkdv_sum), dim3(kBThreads), 0, st, a);
     a.T = (params->fwd.seqlen_q + 127) / 128;
     hipLaunchKernelGGL(plan.k.dq, dim3(plan.grid_dq), dim3(kBThreads), 0, st, a);
