@@ -187,7 +187,10 @@ struct Ops {
         const int tr_row = 4 * (lane >> 5) + ((lane & 15) >> 2);
         const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
         const uint16_t* p0 = tile + (r0 + tr_row) * st + c0 + tr_col;
-        const uint16_t* p1 = p0 + 8 * st;
+        return load_tr_rows(p0, p0 + 8 * st);
+    }
+    // the same from this lane's two addresses (row tr_row and tr_row + 8)
+    __device__ static __forceinline__ op_t load_tr_rows(const uint16_t* p0, const uint16_t* p1) {
         if constexpr (IS_BF16) {
             typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 v4;
             typedef __attribute__((address_space(3))) v4* lp;
@@ -557,15 +560,24 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
     constexpr int DS = DP / 16, DB = DP / 32;
     constexpr int NT = kB8Threads;
     constexpr int BQ = 64;       // query rows per step (two sub-blocks)
-    constexpr int ST = DP + 8;   // LDS row stride (elements) of every tile
+    constexpr int ST = DP + 8;   // LDS row stride (elements) of the K / V tiles
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
+    // Staged Q / dO rows start at chunk 20*row + (row/4)%4 (16-byte chunks):
+    // the start's residue mod 16 chunks (the 64 banks) is 4*(row%4) +
+    // (row/4)%4, distinct over 16 consecutive rows, so the row reads (16 rows,
+    // one chunk each per 256-byte pass) and the transposed reads (4 rows x 4
+    // chunks per pass) both hit 16 distinct 4-bank groups; rows 16 apart
+    // differ by a constant 2560 elements and rows 8 apart (within 4-row
+    // groups 0/1 of each 16) by 1296.
+    constexpr int QT = (20 * BQ + 4) * 8;  // elements per staged Q / dO tile
+    auto rstart = [](int row) { return (20 * row + ((row >> 2) & 3)) * 8; };
     constexpr int SCH = (BQ * CPR + NT - 1) / NT;   // staged chunks per thread and tensor
     constexpr int KCH = (128 * CPR + NT - 1) / NT;  // K (and V) chunks per thread
     // K rows [0, 128) then V rows; reused for the pair sums at the end
     __shared__ __attribute__((aligned(16))) uint16_t kv_s[2 * 128 * ST];
     static_assert(sizeof(kv_s) >= 4 * DB * 16 * 64 * sizeof(float), "pair-sum buffer");
-    __shared__ __attribute__((aligned(16))) uint16_t q_s[2][BQ * ST];
-    __shared__ __attribute__((aligned(16))) uint16_t do_s[2][BQ * ST];
+    __shared__ __attribute__((aligned(16))) uint16_t q_s[2][QT];
+    __shared__ __attribute__((aligned(16))) uint16_t do_s[2][QT];
     __shared__ __attribute__((aligned(16))) float lse_s[2][BQ];
     __shared__ __attribute__((aligned(16))) float ds_s[2][BQ];
 
@@ -631,7 +643,7 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
         const bool in = cc < BQ * CPR && col < D;
         qoff[i] = in ? (uint32_t)(((int64_t)row * f.qs + col) * 2) : 0x80000000u;
         dooff[i] = in ? (uint32_t)(((int64_t)row * a.dos + col) * 2) : 0x80000000u;
-        soff[i] = row * ST + col;
+        soff[i] = rstart(row) + col;
     }
     float lreg = INFINITY, dreg = 0.f;
     auto gload = [&](int step) {
@@ -675,6 +687,12 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
     const uint16_t* kbase = kv_s + (32 * kw + l32) * ST + 8 * half;  // this lane's K row
     const uint16_t* vbase = kbase + 128 * ST;                         // and V row
     const int wk0 = k0 + kw * 32;
+    // this lane's staged-row offsets: row 32*sb + l32 (A operands of S, dP)
+    // and, for the transposed reads, row 32*sb + tr_row, column tr_col
+    const int rq = rstart(32 * sb + l32) + 8 * half;
+    const int tr_row = 4 * half + ((lane & 15) >> 2);
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int rt = rstart(32 * sb + tr_row) + tr_col;
     for (int step = 0; step < nsteps; ++step) {
         const int buf = step & 1;
         if (step + 1 < nsteps) gload(step + 1);  // in flight during this step's MFMAs
@@ -699,12 +717,11 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sacc[4 * g + i] = 0.f;
         }
-        const int row = 32 * sb + l32;
 #pragma unroll
         for (int s = 0; s < DS; ++s) {
-            const op_t qa = *reinterpret_cast<const op_t*>(qsb + row * ST + 16 * s + 8 * half);
+            const op_t qa = *reinterpret_cast<const op_t*>(qsb + rq + 16 * s);
             const op_t kf = *reinterpret_cast<const op_t*>(kbase + 16 * s);
-            const op_t da = *reinterpret_cast<const op_t*>(dosb + row * ST + 16 * s + 8 * half);
+            const op_t da = *reinterpret_cast<const op_t*>(dosb + rq + 16 * s);
             const op_t vf = *reinterpret_cast<const op_t*>(vbase + 16 * s);
             sacc = O::mfma(qa, kf, sacc);
             dpacc = O::mfma(da, vf, dpacc);
@@ -753,8 +770,9 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
             const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const op_t dot = O::load_tr(dosb, ST, 32 * sb + 16 * st, 32 * db, lane);
-                const op_t qt = O::load_tr(qsb, ST, 32 * sb + 16 * st, 32 * db, lane);
+                const int o = rt + 2560 * st + 32 * db;
+                const op_t dot = O::load_tr_rows(dosb + o, dosb + o + 1296);
+                const op_t qt = O::load_tr_rows(qsb + o, qsb + o + 1296);
                 dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
                 dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
             }
