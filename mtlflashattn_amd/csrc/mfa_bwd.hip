@@ -59,6 +59,10 @@ namespace {
 #ifndef MFA_BWD_DKDV8
 #define MFA_BWD_DKDV8 1
 #endif
+// software-pipelined LDS operand reads in the eight-wavefront dK/dV kernel
+#ifndef MFA_BWD_PREFETCH
+#define MFA_BWD_PREFETCH 1
+#endif
 // 32-key blocks per dQ step (four: measured 17 % slower at D=128)
 #ifndef MFA_BWD_DQ_NKB
 #define MFA_BWD_DQ_NKB 2
@@ -717,15 +721,42 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sacc[4 * g + i] = 0.f;
         }
+        // operand fragments are read one MFMA pair ahead (the sched_barriers
+        // keep the compiler from sinking each read to just before its MFMA,
+        // which exposed the LDS latency at every pair)
+        op_t fq[2], fk[2], fd[2], fv[2];
+        auto ld_sdp = [&](int s, int i) __attribute__((always_inline)) {
+            fq[i] = *reinterpret_cast<const op_t*>(qsb + rq + 16 * s);
+            fk[i] = *reinterpret_cast<const op_t*>(kbase + 16 * s);
+            fd[i] = *reinterpret_cast<const op_t*>(dosb + rq + 16 * s);
+            fv[i] = *reinterpret_cast<const op_t*>(vbase + 16 * s);
+        };
+        if constexpr (MFA_BWD_PREFETCH) {
+            ld_sdp(0, 0);
+            static_for<DS>([&](auto sc) __attribute__((always_inline)) {
+                constexpr int s = decltype(sc)::value;
+                if constexpr (s + 1 < DS) ld_sdp(s + 1, (s + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                sacc = O::mfma(fq[s & 1], fk[s & 1], sacc);
+                dpacc = O::mfma(fd[s & 1], fv[s & 1], dpacc);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        } else {
 #pragma unroll
-        for (int s = 0; s < DS; ++s) {
-            const op_t qa = *reinterpret_cast<const op_t*>(qsb + rq + 16 * s);
-            const op_t kf = *reinterpret_cast<const op_t*>(kbase + 16 * s);
-            const op_t da = *reinterpret_cast<const op_t*>(dosb + rq + 16 * s);
-            const op_t vf = *reinterpret_cast<const op_t*>(vbase + 16 * s);
-            sacc = O::mfma(qa, kf, sacc);
-            dpacc = O::mfma(da, vf, dpacc);
+            for (int s = 0; s < DS; ++s) {
+                ld_sdp(s, 0);
+                sacc = O::mfma(fq[0], fk[0], sacc);
+                dpacc = O::mfma(fd[0], fv[0], dpacc);
+            }
         }
+        // the first dV/dK fragments, read before the vector work below
+        op_t fdo[2], fqt[2];
+        auto ld_dvdk = [&](int idx, int i) __attribute__((always_inline)) {
+            const int o = rt + 2560 * (idx / DB) + 32 * (idx % DB);
+            fdo[i] = O::load_tr_rows(dosb + o, dosb + o + 1296);
+            fqt[i] = O::load_tr_rows(qsb + o, qsb + o + 1296);
+        };
+        if constexpr (MFA_BWD_PREFETCH) ld_dvdk(0, 0);
         // P and dS rounded to 16 bits (register r is query qs0 + acc_row(r) +
         // 4*half); sub-blocks whose 32 x 32 pairs are all valid skip the masks
         uint32_t pw[8], dw[8];
@@ -764,17 +795,28 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
             probs(std::true_type{});
         // dV^T += dO^T P, dK^T += Q^T dS (k-slots = query rows of accumulator
         // registers 8*st..8*st+7)
+        if constexpr (MFA_BWD_PREFETCH) {
+            static_for<2 * DB>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int idx = decltype(ic)::value, st = idx / DB, db = idx % DB;
+                if constexpr (idx + 1 < 2 * DB) ld_dvdk(idx + 1, (idx + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
+                const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
+                dva[db] = O::mfma(fdo[idx & 1], __builtin_bit_cast(op_t, pv), dva[db]);
+                dka[db] = O::mfma(fqt[idx & 1], __builtin_bit_cast(op_t, dsv), dka[db]);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        } else {
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
-            const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
+            for (int st = 0; st < 2; ++st) {
+                const u32x4_t pv = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
+                const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const int o = rt + 2560 * st + 32 * db;
-                const op_t dot = O::load_tr_rows(dosb + o, dosb + o + 1296);
-                const op_t qt = O::load_tr_rows(qsb + o, qsb + o + 1296);
-                dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
-                dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
+                for (int db = 0; db < DB; ++db) {
+                    ld_dvdk(st * DB + db, 0);
+                    dva[db] = O::mfma(fdo[0], __builtin_bit_cast(op_t, pv), dva[db]);
+                    dka[db] = O::mfma(fqt[0], __builtin_bit_cast(op_t, dsv), dka[db]);
+                }
             }
         }
         if (step + 1 < nsteps) swrite(buf ^ 1);  // the other stage was last read before the previous barrier
