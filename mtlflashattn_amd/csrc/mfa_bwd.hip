@@ -1011,7 +1011,8 @@ mfa_bwd_dq_kernel(BArgs a) {
         if (u + 1 < nblk) gload(u + 1);  // in flight during this block's MFMAs
         const uint16_t* ksb = k_s[buf];
         const uint16_t* vsb = v_s[buf];
-        uint32_t dw[NKB][8];
+        // one 32-key block at a time: S^T, dP^T, dS^T, then its dQ products
+        // (operand reads pipelined one MFMA pair ahead, as in the dK/dV kernel)
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             // S^T = K Q^T and dP^T = V dO^T (lane = query, registers = keys)
@@ -1025,16 +1026,39 @@ mfa_bwd_dq_kernel(BArgs a) {
             else
 #pragma unroll
                 for (int r = 0; r < 16; ++r) dpacc[r] = 0.f;
+            op_t fk[2], fv[2];
+            auto ld_kv = [&](int s, int i) __attribute__((always_inline)) {
+                fk[i] = *reinterpret_cast<const op_t*>(ksb + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                fv[i] = *reinterpret_cast<const op_t*>(vsb + (32 * kb + l32) * KST + 16 * s + 8 * half);
+            };
+            if constexpr (MFA_BWD_PREFETCH) {
+                ld_kv(0, 0);
+                static_for<DS>([&](auto sc) __attribute__((always_inline)) {
+                    constexpr int s = decltype(sc)::value;
+                    if constexpr (s + 1 < DS) ld_kv(s + 1, (s + 1) & 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    sacc = O::mfma(fk[s & 1], qf[s], sacc);
+                    dpacc = O::mfma(fv[s & 1], dof[s], dpacc);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            } else {
 #pragma unroll
-            for (int s = 0; s < DS; ++s) {
-                const op_t ka = *reinterpret_cast<const op_t*>(ksb + (32 * kb + l32) * KST + 16 * s + 8 * half);
-                const op_t va = *reinterpret_cast<const op_t*>(vsb + (32 * kb + l32) * KST + 16 * s + 8 * half);
-                sacc = O::mfma(ka, qf[s], sacc);
-                dpacc = O::mfma(va, dof[s], dpacc);
+                for (int s = 0; s < DS; ++s) {
+                    ld_kv(s, 0);
+                    sacc = O::mfma(fk[0], qf[s], sacc);
+                    dpacc = O::mfma(fv[0], dof[s], dpacc);
+                }
             }
+            // the first K^T fragment, read before the vector work below
+            op_t fkt[2];
+            auto ld_kt = [&](int idx, int i) __attribute__((always_inline)) {
+                fkt[i] = O::load_tr(ksb, KST, 32 * kb + 16 * (idx / DB), 32 * (idx % DB), lane);
+            };
+            if constexpr (MFA_BWD_PREFETCH) ld_kt(0, 0);
             // tiles whose 32 x 32 pairs are all valid skip the masks
             const int kk0 = j + 32 * kb;
             const bool full = wq0 + 31 < Lq && key_lo(f, wq0 + 31 + dq) <= kk0 && key_hi(f, wq0 + dq, Lk) >= kk0 + 31;
+            uint32_t dw[8];
             auto dsrow = [&](auto masked_tag) {
                 constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
@@ -1052,26 +1076,35 @@ mfa_bwd_dq_kernel(BArgs a) {
                         ds2[i] = DFOLD ? p * dpacc[r + i] : p * (dpacc[r + i] - dsum);
                         if constexpr (BIAS) ds2[i] *= dcap;
                     }
-                    dw[kb][r / 2] = O::pack(ds2[0], ds2[1]);
+                    dw[r / 2] = O::pack(ds2[0], ds2[1]);
                 }
             };
             if (full)
                 dsrow(std::false_type{});
             else
                 dsrow(std::true_type{});
-        }
-        // dQ^T += K^T dS^T (k-slots = keys of accumulator registers 8*st..8*st+7)
+            // dQ^T += K^T dS^T (k-slots = keys of accumulator registers 8*st..8*st+7)
+            if constexpr (MFA_BWD_PREFETCH) {
+                static_for<2 * DB>([&](auto ic) __attribute__((always_inline)) {
+                    constexpr int idx = decltype(ic)::value, st = idx / DB, db = idx % DB;
+                    if constexpr (idx + 1 < 2 * DB) ld_kt(idx + 1, (idx + 1) & 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
+                    dqa[db] = O::mfma(fkt[idx & 1], __builtin_bit_cast(op_t, dsv), dqa[db]);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            } else {
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+                for (int st = 0; st < 2; ++st) {
+                    const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const u32x4_t dsv = {dw[kb][4 * st], dw[kb][4 * st + 1], dw[kb][4 * st + 2], dw[kb][4 * st + 3]};
-#pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    const op_t kt = O::load_tr(ksb, KST, 32 * kb + 16 * st, 32 * db, lane);
-                    dqa[db] = O::mfma(kt, __builtin_bit_cast(op_t, dsv), dqa[db]);
+                    for (int db = 0; db < DB; ++db) {
+                        ld_kt(st * DB + db, 0);
+                        dqa[db] = O::mfma(fkt[0], __builtin_bit_cast(op_t, dsv), dqa[db]);
+                    }
                 }
             }
+        }
         if (u + 1 < nblk) swrite(buf ^ 1);
         __syncthreads();
     }
