@@ -356,7 +356,10 @@ def main():
     peak = PEAK_TFLOPS[c["dtype"]]
     achieved = c["algo"] / (kernel_ms / 1e3) / 1e12
     if args.backward:
-        kname = "mfa_bwd_dsum + mfa_bwd_dkdv + mfa_bwd_dq"
+        # (the eight-wavefront dK/dV kernel above head dim 64; GQA adds the partial-sum kernel)
+        dkdv = "mfa_bwd_dkdv8" if c["D"] > 64 else "mfa_bwd_dkdv"
+        grouped = c["q"].shape[-2] != c["k"].shape[-2]
+        kname = f"mfa_bwd_dsum + {dkdv}" + (" + mfa_bwd_dkdv_sum" if grouped else "") + " + mfa_bwd_dq"
     elif c["varlen"] is not None:
         info = None
         kname = "mfa_fwd16 (varlen)"
@@ -391,8 +394,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kname,
                      "kernel_ms": round(kernel_ms, 4),
-                     "note": "algorithmic FLOPs (4*D per valid (query,key) pair) / mean launch time "
-                             "(HIP events over the K back-to-back timed launches)"},
+                     "note": f"algorithmic FLOPs ({'10' if args.backward else '4'}*D per valid (query,key) pair) "
+                             "/ mean launch time (HIP events over the K back-to-back timed launches)"},
     }
     if "hbm_bytes" in c:
         gbs = c["hbm_bytes"] / (kernel_ms / 1e3) / 1e9
