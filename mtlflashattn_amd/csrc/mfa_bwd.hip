@@ -63,6 +63,11 @@ namespace {
 #ifndef MFA_BWD_PREFETCH
 #define MFA_BWD_PREFETCH 1
 #endif
+// grouped-query dK/dV: one workgroup per query head into fp32 partials
+// (summed afterwards) rather than one per K/V head looping over its group
+#ifndef MFA_BWD_HEAD_SPLIT
+#define MFA_BWD_HEAD_SPLIT 1
+#endif
 // 32-key blocks per dQ step (four: measured 17 % slower at D=128)
 #ifndef MFA_BWD_DQ_NKB
 #define MFA_BWD_DQ_NKB 2
@@ -1281,7 +1286,7 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     // each workgroup loops over its K/V head's query heads.
     const int R = p->heads_q / p->heads_kv;
     const int64_t part = (int64_t)a.Ukv * p->seqlen_k * dp * 4;  // one group's dK (or dV) partials
-    a.G = (R > 1 && 2 * R * part <= ((int64_t)2 << 30)) ? R : 1;
+    a.G = (MFA_BWD_HEAD_SPLIT && R > 1 && 2 * R * part <= ((int64_t)2 << 30)) ? R : 1;
     a.ws_ld = dp;
     const int64_t part_bytes = a.G > 1 ? 2 * a.G * part : 0;
     plan->ws_bytes = plan->empty ? 0 : plan->dsum_bytes + part_bytes;
