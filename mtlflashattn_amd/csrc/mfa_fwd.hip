@@ -720,7 +720,15 @@ mfa_fwd16_kernel(KArgs a) {
         tile /= a.nsplit;
     }
     const SeqView sv = seq_view<2>(a, b, hq);
-    const int q0 = tile * BM;
+    // Head-packed tiles (a.hpack = R > 1, grouped-query calls): the tile
+    // holds PM positions of each of the R query heads of one K/V head,
+    // head-major (tile row = head * PM + position); wave w takes head
+    // w / (kWaves / R) at position block w % (kWaves / R), so it still holds
+    // QB * 32 aligned positions of one head and its rows' arithmetic equals
+    // the unpacked tile's.
+    const int hpk = EXACT ? 1 : a.hpack;
+    const int PM = BM / hpk;  // positions per tile
+    const int q0 = tile * PM;
     if (q0 >= sv.Lq) return;
     // a varlen call mixing single-row sequences with longer ones: the
     // exact-row kernel's launch takes the single-row ones, this one the rest
@@ -733,8 +741,10 @@ mfa_fwd16_kernel(KArgs a) {
     const int Lq = sv.Lq, Lk = sv.Lk, D = a.D;
     const int dq = Lk - Lq;
 
-    const int wq0 = q0 + wave * QB * 32;  // first query row of this wavefront
-    op_t qf[QB][DS];                       // Q as MFMA B operands (filled below)
+    const int wph = kWaves / hpk;                      // waves per head
+    const int hl = wave / wph;                         // this wave's head inside the tile
+    const int wq0 = q0 + (wave - hl * wph) * QB * 32;  // first query row of this wavefront
+    op_t qf[QB][DS];                                   // Q as MFMA B operands (filled below)
 
 
     // ---- per-lane query state
@@ -744,7 +754,7 @@ mfa_fwd16_kernel(KArgs a) {
         rs[qb].center = wq0 + 32 * qb + l32 + dq;
         rs[qb].lo = key_lo(a, rs[qb].center);
         rs[qb].hi = key_hi(a, rs[qb].center, Lk);
-        rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq] : 0.f;
+        rs[qb].slope = a.alibi ? a.alibi[b * a.alibi_bstride + hq * hpk + hl] : 0.f;
         row_reset(rs[qb]);
     }
     f32x16_t o[QB][DB];
@@ -765,7 +775,7 @@ mfa_fwd16_kernel(KArgs a) {
     const float tau_c = tau / c;
 
     // ---- key range of the workgroup and of this wavefront
-    const int qlast = min(q0 + BM, Lq) - 1;
+    const int qlast = min(q0 + PM, Lq) - 1;
     const int klo = key_lo(a, q0 + dq);
     const int khi = key_hi(a, qlast + dq, Lk);
     int jbeg = (klo / BN) * BN;
@@ -1118,9 +1128,10 @@ mfa_fwd16_kernel(KArgs a) {
     // ---- Q tile -> LDS (coalesced) -> registers as MFMA B operands
     for (int c = tid; c < BM * CPR; c += kThreads) {
         const int row = c / CPR, col = (c % CPR) * 8;
+        const int h = row / PM, pos = q0 + row - h * PM;
         u32x4_t val = {0, 0, 0, 0};
-        if (q0 + row < Lq && col < D)
-            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)(q0 + row) * a.qs + col) * 2);
+        if (pos < Lq && col < D)
+            val = *reinterpret_cast<const u32x4_t*>(sv.q + ((int64_t)h * a.qh1 + (int64_t)pos * a.qs + col) * 2);
         *reinterpret_cast<u32x4_t*>(smem + row * KST + col) = val;
     }
     __syncthreads();
@@ -1189,11 +1200,17 @@ mfa_fwd16_kernel(KArgs a) {
         __syncthreads();
     }
 
-    if (a.nsplit > 1)
+    if (a.nsplit > 1) {
         store_partial<QB, DB>(a, Lq, b * a.Hq + hq, split, o, rs, c, wq0, lane);
-    else  // (the loop's last barrier released the LDS)
-        store_out_rows<QB, DB, IS_BF16, KST>(a, sv, o, rs, wq0, lane, c,
+    } else {  // (the loop's last barrier released the LDS)
+        SeqView svh = sv;  // this wave's head: its O and lse rows
+        if (!EXACT && hl != 0) {
+            svh.o += (int64_t)hl * a.oh1 * (a.out_f32 ? 4 : 2);
+            if (svh.lse) svh.lse += (int64_t)hl * a.lse_h1;
+        }
+        store_out_rows<QB, DB, IS_BF16, KST>(a, svh, o, rs, wq0, lane, c,
                                              smem + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * QB * 32 * KST);
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -2155,6 +2172,10 @@ KernelCfg cfg32(const char* name, bool paged) {
 #ifndef MFA_PP_HEAD_PACK
 #define MFA_PP_HEAD_PACK 1
 #endif
+// ... and so do the 4-wavefront 16-bit tiles (2 or 4 heads)
+#ifndef MFA_4W_HEAD_PACK
+#define MFA_4W_HEAD_PACK 1
+#endif
 // paged K/V (block_table) runs on the 256-row and fp32 kernels only
 template <bool IS_BF16, bool BIAS>
 KernelCfg select16(int dp, bool fills_chip, bool paged, bool pp256) {
@@ -2434,7 +2455,6 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     // short or single-row queries run faster on the 4-wavefront kernel.
     const int64_t rows512 = (int64_t)((p->seqlen_q + 511) / 512) * 512;
     const int64_t rows256 = (int64_t)((p->seqlen_q + 255) / 256) * 256;
-    const int64_t rows128 = (int64_t)((p->seqlen_q + 127) / 128) * 128;
     const int64_t units = (int64_t)p->batch * p->heads_q;
     bool fills_chip = pp_hint;
     if (p->tile_hint == MFA_TILE_AUTO) {
@@ -2453,13 +2473,29 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             // non-causal threshold rises to 12 tiles (8 lengths in [863, 3501]
             // at Hq=32 Hkv=8: non-causal 798 vs 870 us; 32 lengths in
             // [128, 2048]: 828 vs 751).
-            const int64_t t256 = rows256 / 256;
+            // A grouped-query call with 2, 4 or 8 query heads per K/V head
+            // packs them into each tile (256 / R positions per ping-pong
+            // tile): there rows of >= 2048 positions go to the ping-pong
+            // tiles, causal or not, varlen or dense (measured at Hq=32 Hkv=8
+            // D=128 on packed tiles, ping-pong vs 4-wavefront: config 4's 8
+            // varlen lengths in [863, 3501] causal 474 vs 516 us, non-causal
+            // 802 vs 868; 16 lengths in [256, 4096] 919 vs 997 and 1610 vs
+            // 1770; 32 in [128, 2048] 623 vs 624 and 991 vs 1065; 64 in [64,
+            // 1024] 389 vs 344 and 521 vs 496; B=4 L=2048 causal 162 vs 171).
+            const int64_t Rq = p->heads_kv > 0 ? p->heads_q / p->heads_kv : 1;
+            const bool packs = MFA_PP_HEAD_PACK && (Rq == 2 || Rq == 4 || Rq == 8);
+            const int64_t pos_pp = packs ? 256 / Rq : 256;  // positions per ping-pong tile
+            const int64_t pos_4w = MFA_4W_HEAD_PACK && (Rq == 2 || Rq == 4) ? 128 / Rq : 128;
+            const int64_t rows_pp = (p->seqlen_q + pos_pp - 1) / pos_pp * pos_pp;
+            const int64_t rows_4w = (p->seqlen_q + pos_4w - 1) / pos_4w * pos_4w;
+            const int64_t units_pp = packs ? (int64_t)p->batch * p->heads_kv : units;
+            const int64_t t256 = rows_pp / pos_pp;
             const int64_t inf = INT64_MAX / 4;
             const int64_t left = p->window_left >= 0 ? p->window_left : inf;
             const int64_t right = p->causal ? 0 : p->window_right >= 0 ? p->window_right : inf;
             const bool windowed = p->window_left >= 0 || p->window_right >= 0;
-            const int64_t min_tiles = p->causal ? 16 : p->cu_seqlens_q ? 12 : 8;
-            fills_chip = units * t256 >= geom.cus && 4 * rows256 <= 5 * rows128 && t256 >= min_tiles &&
+            const int64_t min_tiles = packs ? (2048 + pos_pp - 1) / pos_pp : p->causal ? 16 : p->cu_seqlens_q ? 12 : 8;
+            fills_chip = units_pp * t256 >= geom.cus && 4 * rows_pp <= 5 * rows_4w && t256 >= min_tiles &&
                          (!windowed || (!bias && left + right + 1 >= 2048));
         } else
             fills_chip = units * (rows512 / 512) >= geom.cus && 4 * rows512 <= 5 * rows256;
@@ -2620,7 +2656,12 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     a.oh1 = a.oh;
     a.lse_h1 = a.lse_h;
     const int R = p->heads_q / p->heads_kv;
-    if (MFA_PP_HEAD_PACK && plan->cfg.threads == 8 * 64 && (R == 2 || R == 4 || R == 8)) {
+    // The 4-wavefront 16-bit kernel packs 2 or 4 heads the same way (one or
+    // two wavefronts per head), except for split-KV and paged calls.
+    const bool pack_pp = MFA_PP_HEAD_PACK && plan->cfg.threads == 8 * 64 && (R == 2 || R == 4 || R == 8);
+    const bool pack_4w = MFA_4W_HEAD_PACK && din != MFA_DTYPE_F32 && !exact_call && !tiny_keys && !paged &&
+                         split_keys == 0 && plan->cfg.threads == kThreads && (R == 2 || R == 4);
+    if (pack_pp || pack_4w) {
         a.hpack = R;
         a.Hq = p->heads_kv;
         a.qh = p->q_head_stride * R;
@@ -2641,6 +2682,14 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         a.grouped = 1;
         a.xcd_shift = xshift;
         a.tile_major = (p->causal || p->window_left >= 0 || p->window_right >= 0) ? 1 : 0;
+        // Head-packed varlen tiles run unit-major: a packed tile reads its K/V
+        // once for its R heads, so the L2 reuse that tile-major order gets
+        // from the R heads of one (sequence, K/V head) running side by side is
+        // gone, and tiles of sequences of different lengths interleaved on an
+        // XCD evict each other's K/V (config 4: 644 vs 494 us on the
+        // 4-wavefront tiles, 617 vs 469 on the ping-pong ones).  Dense calls
+        // keep tile-major order (B=4 L=2048 Hq=32 Hkv=8 causal 169 vs 173 us).
+        if (a.hpack > 1 && p->cu_seqlens_q) a.tile_major = 0;
         a.upx = (int32_t)(G / X) * (a.Hq / p->heads_kv);
         plan->grid = X * a.upx * a.T;
     } else {

@@ -221,7 +221,9 @@ def test_launch_geometry_of_the_baseline_configs(lib):
 
 def test_varlen_d128_kernel_choice(lib):
     # varlen calls give the longest sequence only: at head dim 128 the
-    # ping-pong tiles need >= 12 tiles of 256 rows non-causal, 16 causal
+    # ping-pong tiles need >= 12 tiles of 256 rows non-causal, 16 causal;
+    # grouped-query calls whose tiles pack 2, 4 or 8 query heads need rows
+    # of >= 2048 positions
     def varlen(nseq, longest, Hq, Hkv, causal):
         p = good_params(B=nseq, L=longest, H=Hq, Hkv=Hkv, D=128)
         p.q_batch_stride = p.k_batch_stride = p.v_batch_stride = p.o_batch_stride = 0
@@ -229,8 +231,11 @@ def test_varlen_d128_kernel_choice(lib):
         p.causal = int(causal)
         return _hip.launch_info(p).kernel_name
     assert varlen(8, 3501, 32, 8, False).startswith(b"mfa_fwd16pp<bf16,d128")
-    assert varlen(8, 3501, 32, 8, True).startswith(b"mfa_fwd16<bf16,d128")
-    assert varlen(32, 2048, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")
+    assert varlen(8, 3501, 32, 8, True).startswith(b"mfa_fwd16pp<bf16,d128")
+    assert varlen(32, 2048, 32, 8, False).startswith(b"mfa_fwd16pp<bf16,d128")
+    assert varlen(64, 1024, 32, 8, True).startswith(b"mfa_fwd16<bf16,d128")
+    assert varlen(64, 1024, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")
+    assert varlen(8, 3501, 16, 16, True).startswith(b"mfa_fwd16<bf16,d128")  # one head per K/V head: 14 < 16
     assert varlen(4, 8192, 16, 16, True).startswith(b"mfa_fwd16pp<bf16,d128")
 
 

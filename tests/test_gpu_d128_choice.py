@@ -1,7 +1,8 @@
 """Head dim 128 calls that the automatic choice sends to the ping-pong tiles
 because their key ranges are long: sliding windows of >= 2048 keys without a
 soft-cap / ALiBi transform, and varlen calls whose longest sequence has >= 12
-tiles of 256 rows (16 when causal).  Each case checks the kernel the library
+tiles (16 when causal) -- of 256 rows, or of 256 / R positions when the
+tiles pack R = 2, 4 or 8 query heads of one K/V head.  Each case checks the kernel the library
 picks (launch_info / the plan's name) and the result against the oracle
 (_kernel.py:1188-1207's mask order), in the fp32 parity
 output and the 16-bit output; the 4-wavefront kernel on the same call meets
@@ -67,9 +68,18 @@ def test_long_varlen_non_causal_takes_the_pingpong_tiles(dtype, monkeypatch):
     out32 = _kernel.forward_varlen(q, k, v, cu_q, cu_k, max(lens), max(lens), default_scale(128), False,
                                    out_dtype=torch.float32)
     assert_parity(out32, ref, dtype, "varlen non-causal fp32 out")
-    # causal: 14 tiles are below the causal threshold (16): 4-wavefront kernel
+    # causal: 4 query heads per K/V head pack into each ping-pong tile, so
+    # the longest sequence has 55 tiles of 64 positions (>= 16): ping-pong
     ran.clear()
     outc = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens), max(lens), causal=True)
-    assert ran and ran[-1].startswith(b"mfa_fwd16<"), ran
+    assert ran and ran[-1].startswith(b"mfa_fwd16pp<"), ran
     refc = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=True)
-    assert_output(outc, refc, dtype, "varlen causal (4-wave)")
+    assert_output(outc, refc, dtype, "varlen causal GQA (ping-pong)")
+    # the same lengths with one query head per K/V head: 14 tiles of 256 rows
+    # are below the causal threshold (16), so the 4-wavefront kernel
+    qm, km, vm, _, _ = make_varlen(lens, lens, 4, 4, 128, dtype, seed=45)
+    ran.clear()
+    outm = mfa.flash_attn_varlen_func(qm, km, vm, cu_q, cu_k, max(lens), max(lens), causal=True)
+    assert ran and ran[-1].startswith(b"mfa_fwd16<"), ran
+    refm = chunked.flash_attn_varlen_func(qm.cpu(), km.cpu(), vm.cpu(), cu_q.cpu(), cu_k.cpu(), causal=True)
+    assert_output(outm, refm, dtype, "varlen causal (4-wave)")

@@ -1,6 +1,7 @@
-"""Ping-pong tiles that pack the query heads of one K/V head (grouped-query
-calls with 2, 4 or 8 query heads per K/V head): the heads share a tile and
-its K/V stream, each over 1/R of the tile's rows at the same positions.
+"""Tiles that pack the query heads of one K/V head (grouped-query calls with
+2, 4 or 8 query heads per K/V head on the ping-pong tiles, 2 or 4 on the
+4-wavefront tiles): the heads share a tile and its K/V stream, each over 1/R
+of the tile's rows at the same positions.
 GQA head mapping (metal_flash_attn/_kernel.py:54, hkv = hq / (Hq/Hkv)) must
 stay bit-exact: every row equals the same call with K/V repeated per query
 head (where each head has tiles of its own), outputs and lse alike, and
@@ -18,10 +19,10 @@ from gpu_util import DEV, assert_output, assert_parity, default_scale, make_qkv,
 
 pytestmark = pytest.mark.gpu
 
-PP = [_hip.MFA_TILE_PINGPONG, _hip.MFA_TILE_PINGPONG256]
+TILES = [_hip.MFA_TILE_256, _hip.MFA_TILE_PINGPONG, _hip.MFA_TILE_PINGPONG256]
 
 
-@pytest.fixture(params=PP, ids=["pingpong", "pingpong256"])
+@pytest.fixture(params=TILES, ids=["4wave", "pingpong", "pingpong256"])
 def pp(request, monkeypatch):
     monkeypatch.setattr(_kernel, "_TILE_HINT", request.param)
     return request.param
@@ -102,3 +103,18 @@ def test_launch_geometry():
         _kernel._TILE_HINT = _hip.MFA_TILE_AUTO
     assert info.kernel_name.startswith(b"mfa_fwd16pp<bf16,d128")
     assert info.grid_x == 4 * 4096 // 64  # K/V heads x position tiles
+
+
+def test_launch_geometry_four_wave():
+    # the same call on 4-wavefront tiles: 4 heads x 32 positions per 128-row
+    # tile at D=128, 4 heads x 64 positions per 256-row tile at D=64
+    _kernel._TILE_HINT = _hip.MFA_TILE_256
+    try:
+        for D, pos in ((128, 32), (64, 64)):
+            q = torch.empty(1, 4096, 16, D, dtype=torch.bfloat16)
+            k = torch.empty(1, 4096, 4, D, dtype=torch.bfloat16)
+            info = _kernel.launch_info(q, k, k)
+            assert info.kernel_name.startswith(b"mfa_fwd16<bf16,d%d" % D), info.kernel_name
+            assert info.grid_x == 4 * 4096 // pos, (D, info.grid_x)
+    finally:
+        _kernel._TILE_HINT = _hip.MFA_TILE_AUTO
