@@ -361,8 +361,9 @@ def main():
         grouped = c["q"].shape[-2] != c["k"].shape[-2]
         kname = f"mfa_bwd_dsum + {dkdv}" + (" + mfa_bwd_dkdv_sum" if grouped else "") + " + mfa_bwd_dq"
     elif c["varlen"] is not None:
-        info = None
-        kname = "mfa_fwd16 (varlen)"
+        cu, mx = c["varlen"]
+        info = _kernel.launch_info_varlen(c["q"], c["k"], cu.shape[0] - 1, mx, mx, causal=c["kw"].get("causal", False))
+        kname = info.kernel_name.decode() + " (varlen)"
     else:
         info = _kernel.launch_info(c["q"], c["k"], c["v"], causal=c["kw"].get("causal", False),
                                    softcap=c["kw"].get("softcap", 0.0),

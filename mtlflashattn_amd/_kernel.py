@@ -664,3 +664,31 @@ def launch_info(q, k, v, causal=False, softcap=0.0, alibi=False, window_left=-1,
         hint = _hip.MFA_TILE_AUTO
     p.tile_hint = hint
     return _hip.launch_info(p)
+
+
+def launch_info_varlen(q, k, nseq, max_seqlen_q, max_seqlen_k, causal=False, softcap=0.0, alibi=False,
+                       window_left=-1, window_right=-1):
+    """launch_info for a varlen call: q [total_q, Hq, D], k [total_k, Hkv, D],
+    nseq sequences of at most max_seqlen_q / max_seqlen_k rows (the plan
+    reads no prefix sums)."""
+    Hq, D = q.shape[1], q.shape[2]
+    Hkv = k.shape[1]
+    p = _hip.MfaFwdParams()
+    p.q = p.k = p.v = p.o = 256  # placeholder aligned addresses: nothing is read
+    p.q_seq_stride, p.q_head_stride = Hq * D, D
+    p.k_seq_stride, p.k_head_stride = Hkv * D, D
+    p.v_seq_stride, p.v_head_stride = Hkv * D, D
+    p.o_seq_stride, p.o_head_stride = Hq * D, D
+    p.batch, p.heads_q, p.heads_kv = nseq, Hq, Hkv
+    p.seqlen_q, p.seqlen_k, p.head_dim = max_seqlen_q, max_seqlen_k, -(-D // 8) * 8
+    p.cu_seqlens_q = p.cu_seqlens_k = 256
+    p.scale = 1.0
+    p.softcap = float(softcap)
+    p.window_left, p.window_right, p.causal = window_left, window_right, int(causal)
+    p.alibi_slopes = 256 if alibi else None
+    p.dtype_in = p.dtype_out = _hip.DTYPE_CODES[q.dtype]
+    hint = _TILE_HINT
+    if q.dtype == torch.float32 or (hint in _PP_HINTS and not _pp_head_dim_ok(p.head_dim)):
+        hint = _hip.MFA_TILE_AUTO
+    p.tile_hint = hint
+    return _hip.launch_info(p)

@@ -237,6 +237,11 @@ def test_varlen_d128_kernel_choice(lib):
     assert varlen(64, 1024, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")
     assert varlen(8, 3501, 16, 16, True).startswith(b"mfa_fwd16<bf16,d128")  # one head per K/V head: 14 < 16
     assert varlen(4, 8192, 16, 16, True).startswith(b"mfa_fwd16pp<bf16,d128")
+    # the Python helper plans the same call (config 4's geometry)
+    q = torch.empty(18373, 32, 128, dtype=torch.bfloat16)
+    k = torch.empty(18373, 8, 128, dtype=torch.bfloat16)
+    info = _kernel.launch_info_varlen(q, k, 8, 3501, 3501, causal=True)
+    assert info.kernel_name.startswith(b"mfa_fwd16pp<bf16,d128") and info.block_x == 512
 
 
 def test_oversized_grids_are_rejected_not_wrapped(lib):
