@@ -68,6 +68,11 @@ namespace {
 #ifndef MFA_BWD_HEAD_SPLIT
 #define MFA_BWD_HEAD_SPLIT 1
 #endif
+// staged rows of the four-wavefront dK/dV tiles and the dQ kernel's K/V
+// tiles permuted within 16-row groups (bank-conflict-free transposed reads)
+#ifndef MFA_BWD_PERM
+#define MFA_BWD_PERM 1
+#endif
 // 32-key blocks per dQ step (four: measured 17 % slower at D=128)
 #ifndef MFA_BWD_DQ_NKB
 #define MFA_BWD_DQ_NKB 2
@@ -160,6 +165,14 @@ __device__ __forceinline__ KView k_view(const BArgs& a, int b, int hkv) {
     return s;
 }
 
+// Row permutation within 16-row groups for padded tiles of row stride
+// D + 8 elements (D/8 + 1 16-byte chunks, = 1 mod 4): row r is stored at
+// LDS row prow(r) = 4*(r mod 4) + (r/4) mod 4 of its group.  The 16 rows a
+// row read covers per pass then start in 16 distinct 4-bank groups (any odd
+// stride permutes the residues), and the 4 rows x 4 chunks of a transposed
+// read's pass fall on 4*(r mod 4) + chunk + const: 16 distinct groups too.
+__device__ __forceinline__ int prow(int r) { return (r & ~15) | ((r & 3) << 2) | ((r >> 2) & 3); }
+
 template <bool IS_BF16>
 struct Ops {
     typedef typename std::conditional<IS_BF16, bf16x8_t, f16x8_t>::type op_t;
@@ -197,6 +210,14 @@ struct Ops {
         const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
         const uint16_t* p0 = tile + (r0 + tr_row) * st + c0 + tr_col;
         return load_tr_rows(p0, p0 + 8 * st);
+    }
+    // load_tr on a tile whose rows are stored permuted within 16-row groups
+    // (row r at LDS row prow(r)); r0 is a multiple of 16
+    __device__ static __forceinline__ op_t load_tr_perm(const uint16_t* tile, int st, int r0, int c0, int lane) {
+        const int tr_row = 4 * (lane >> 5) + ((lane & 15) >> 2);
+        const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const uint16_t* base = tile + r0 * st + c0 + tr_col;
+        return load_tr_rows(base + prow(tr_row) * st, base + prow(tr_row + 8) * st);
     }
     // the same from this lane's two addresses (row tr_row and tr_row + 8)
     __device__ static __forceinline__ op_t load_tr_rows(const uint16_t* p0, const uint16_t* p1) {
@@ -390,7 +411,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         const bool in = cc < BQ * CPR && col < D;
         qoff[i] = in ? (uint32_t)(((int64_t)row * f.qs + col) * 2) : 0x80000000u;
         dooff[i] = in ? (uint32_t)(((int64_t)row * a.dos + col) * 2) : 0x80000000u;
-        soff[i] = row * QST + col;
+        soff[i] = (MFA_BWD_PERM ? prow(row) : row) * QST + col;
     }
     float lreg = INFINITY, dreg = 0.f;
     auto gload = [&](int step) {
@@ -464,8 +485,9 @@ mfa_bwd_dkdv_kernel(BArgs a) {
 #pragma unroll
                 for (int sb = 0; sb < QSB; ++sb) {
                     const int row = 32 * sb + l32;
-                    const op_t qa = *reinterpret_cast<const op_t*>(qsb + row * QST + 16 * s + 8 * half);
-                    const op_t da = *reinterpret_cast<const op_t*>(dosb + row * QST + 16 * s + 8 * half);
+                    const int prw = MFA_BWD_PERM ? prow(row) : row;
+                    const op_t qa = *reinterpret_cast<const op_t*>(qsb + prw * QST + 16 * s + 8 * half);
+                    const op_t da = *reinterpret_cast<const op_t*>(dosb + prw * QST + 16 * s + 8 * half);
                     sacc[sb] = O::mfma(qa, kf[s], sacc[sb]);
                     dpacc[sb] = O::mfma(da, vf[s], dpacc[sb]);
                 }
@@ -525,8 +547,10 @@ mfa_bwd_dkdv_kernel(BArgs a) {
                     const u32x4_t dsv = {dw[4 * st], dw[4 * st + 1], dw[4 * st + 2], dw[4 * st + 3]};
 #pragma unroll
                     for (int db = 0; db < DB; ++db) {
-                        const op_t dot = O::load_tr(dosb, QST, 32 * sb + 16 * st, 32 * db, lane);
-                        const op_t qt = O::load_tr(qsb, QST, 32 * sb + 16 * st, 32 * db, lane);
+                        const op_t dot = MFA_BWD_PERM ? O::load_tr_perm(dosb, QST, 32 * sb + 16 * st, 32 * db, lane)
+                                                      : O::load_tr(dosb, QST, 32 * sb + 16 * st, 32 * db, lane);
+                        const op_t qt = MFA_BWD_PERM ? O::load_tr_perm(qsb, QST, 32 * sb + 16 * st, 32 * db, lane)
+                                                     : O::load_tr(qsb, QST, 32 * sb + 16 * st, 32 * db, lane);
                         dva[db] = O::mfma(dot, __builtin_bit_cast(op_t, pv), dva[db]);
                         dka[db] = O::mfma(qt, __builtin_bit_cast(op_t, dsv), dka[db]);
                     }
@@ -981,7 +1005,7 @@ mfa_bwd_dq_kernel(BArgs a) {
         const bool in = cc < BN * CPR && col < D;
         koff[i] = in ? (uint32_t)(((int64_t)row * f.ks + col) * 2) : 0x80000000u;
         voff[i] = in ? (uint32_t)(((int64_t)row * f.vs + col) * 2) : 0x80000000u;
-        soff[i] = row * KST + col;
+        soff[i] = (MFA_BWD_PERM ? prow(row) : row) * KST + col;
     }
     auto gload = [&](int u) {
         const int j = jbeg + u * BN;
@@ -1033,8 +1057,9 @@ mfa_bwd_dq_kernel(BArgs a) {
                 for (int r = 0; r < 16; ++r) dpacc[r] = 0.f;
             op_t fk[2], fv[2];
             auto ld_kv = [&](int s, int i) __attribute__((always_inline)) {
-                fk[i] = *reinterpret_cast<const op_t*>(ksb + (32 * kb + l32) * KST + 16 * s + 8 * half);
-                fv[i] = *reinterpret_cast<const op_t*>(vsb + (32 * kb + l32) * KST + 16 * s + 8 * half);
+                const int krow = 32 * kb + (MFA_BWD_PERM ? prow(l32) : l32);
+                fk[i] = *reinterpret_cast<const op_t*>(ksb + krow * KST + 16 * s + 8 * half);
+                fv[i] = *reinterpret_cast<const op_t*>(vsb + krow * KST + 16 * s + 8 * half);
             };
             if constexpr (MFA_BWD_PREFETCH) {
                 ld_kv(0, 0);
@@ -1057,7 +1082,8 @@ mfa_bwd_dq_kernel(BArgs a) {
             // the first K^T fragment, read before the vector work below
             op_t fkt[2];
             auto ld_kt = [&](int idx, int i) __attribute__((always_inline)) {
-                fkt[i] = O::load_tr(ksb, KST, 32 * kb + 16 * (idx / DB), 32 * (idx % DB), lane);
+                fkt[i] = MFA_BWD_PERM ? O::load_tr_perm(ksb, KST, 32 * kb + 16 * (idx / DB), 32 * (idx % DB), lane)
+                                      : O::load_tr(ksb, KST, 32 * kb + 16 * (idx / DB), 32 * (idx % DB), lane);
             };
             if constexpr (MFA_BWD_PREFETCH) ld_kt(0, 0);
             // tiles whose 32 x 32 pairs are all valid skip the masks
