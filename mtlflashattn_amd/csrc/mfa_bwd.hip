@@ -1324,6 +1324,22 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     const int R = p->heads_q / p->heads_kv;
     const int64_t part = (int64_t)a.Ukv * p->seqlen_k * dp * 4;  // one group's dK (or dV) partials
     a.G = (MFA_BWD_HEAD_SPLIT && R > 1 && 2 * R * part <= ((int64_t)2 << 30)) ? R : 1;
+    if (a.G > 1 && dp > 64 && MFA_BWD_DKDV8) {
+        // The eight-wavefront dK/dV kernel (one workgroup per CU) needs fewer
+        // workgroups than the partials' traffic is worth: the fewest groups
+        // (a power of two dividing R) that give >= 512 workgroups on dense
+        // calls, 2048 on varlen calls (whose key tiles are counted at the
+        // longest sequence).  Measured at D=128 causal, groups R / 2 / 1
+        // (ms): B=1 L=8192 Hq=32 Hkv=8 2.15 / 2.09 / 2.07, B=2 L=4096
+        // 1.27 / 1.21 / 1.18, B=4 L=2048 Hq=16 Hkv=8 non-causal 0.67 / 0.65 /
+        // 0.61, B=1 L=8192 Hq=32 Hkv=4 2.15 / 2.10 / 2.9, config 4's varlen
+        // batch 1.97 / 1.88 / 1.94.
+        const int64_t ktiles = (p->seqlen_k + 127) / 128;
+        const int64_t target = p->cu_seqlens_q ? 2048 : 512;
+        int g = 1;
+        while (g < R && (int64_t)a.Ukv * g * ktiles < target) g *= 2;
+        if (g < R && R % g == 0) a.G = g;
+    }
     a.ws_ld = dp;
     const int64_t part_bytes = a.G > 1 ? 2 * a.G * part : 0;
     plan->ws_bytes = plan->empty ? 0 : plan->dsum_bytes + part_bytes;

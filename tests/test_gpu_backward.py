@@ -199,6 +199,23 @@ def test_gqa_grads_equal_summed_repeated_heads():
         assert rel_err(g, summed.cpu()) <= GRAD_REL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("B,L,hq,hkv", [(4, 2048, 16, 8), (1, 8192, 16, 4)], ids=["one-group", "two-groups"])
+def test_gqa_head_groups_at_d128(B, L, hq, hkv):
+    # grouped-query dK/dV at head dim 128 with one workgroup per K/V head
+    # looping over its query heads (512 workgroups already) and with two
+    # groups of query heads whose fp32 partials are summed
+    q, k, v = make_qkv(B, L, L, hq, hkv, 128, torch.bfloat16, seed=L + hkv)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(L)).to(DEV, torch.bfloat16)
+    f = lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True)  # noqa: E731
+    r = hq // hkv
+    _, dq, dk, dv = grads_of(f, q, k, v, dout)
+    _, dq_r, dk_r, dv_r = grads_of(f, q, k.repeat_interleave(r, dim=2), v.repeat_interleave(r, dim=2), dout)
+    assert torch.equal(dq, dq_r)
+    for g, rep in ((dk, dk_r), (dv, dv_r)):
+        summed = rep.float().reshape(B, L, hkv, r, 128).sum(3)
+        assert rel_err(g, summed.cpu()) <= GRAD_REL[torch.bfloat16]
+
+
 @pytest.mark.parametrize("dtype", DTYPES16)
 def test_lse_gradient(dtype):
     # loss = sum(out * dout) + sum(lse * dlse): the lse gradient enters as Dsum - dlse
