@@ -12,20 +12,23 @@
 //
 // Three kernels, no atomics (the result does not depend on scheduling):
 //  * mfa_bwd_dsum_kernel: Dsum per query row (fp32), 16 lanes per row.
-//  * mfa_bwd_dkdv_kernel: a workgroup owns 128 keys of one (sequence, K/V
-//    head), 32 per wavefront, with K and V resident in registers as MFMA B
-//    operands.  It walks every query block (32 rows, staged in LDS with their
-//    dO, lse and Dsum) of every query head of the K/V group that can see its
-//    keys.  S = Q K^T and dP = dO V^T come out with lane = key, so P and dS
-//    feed dV^T += dO^T P and dK^T += Q^T dS straight from the accumulators
-//    (rounded to 16 bits), with dO^T / Q^T read from LDS by
+//  * mfa_bwd_dkdv_kernel (head dims up to 64) / mfa_bwd_dkdv8_kernel (above):
+//    a workgroup owns 128 keys of one (sequence, K/V head), 32 per
+//    wavefront, with K and V resident in registers as MFMA B operands (four
+//    wavefronts) or read from LDS (eight wavefronts, two per SIMD: pairs
+//    that own the same keys split each step's query rows and add their
+//    partial sums at the end).  It walks every query block (staged in LDS
+//    with its dO, lse and Dsum) of every query head of its head group that
+//    can see its keys.  S = Q K^T and dP = dO V^T come out with lane = key,
+//    so P and dS feed dV^T += dO^T P and dK^T += Q^T dS straight from the
+//    accumulators (rounded to 16 bits), with dO^T / Q^T read from LDS by
 //    ds_read_b64_tr_b16 -- the same operand scheme as the forward's O^T.
 //  * mfa_bwd_dq_kernel: a workgroup owns 128 query rows, 32 per wavefront,
 //    with Q and dO resident in registers; it walks the key blocks (64 keys,
 //    staged in LDS) its rows can see.  S^T = K Q^T and dP^T = V dO^T give
 //    lane = query, and dQ^T += K^T dS^T takes dS^T from the accumulators.
-// Masks are applied element-wise in every block (the backward is matrix-core
-// bound: four or three GEMMs per tile against a handful of vector ops).
+// Tiles whose query-key pairs are all valid skip the masks; boundary tiles
+// mask element-wise with selects (no branches).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
