@@ -5,7 +5,14 @@
 // states the mask/bias/online-softmax math most plainly) and :1165-1208 (the
 // chunked fp32 torch path, whose results these kernels must reproduce).
 //
-// Design (one kernel family, FA-2 forward, one workgroup = 4 wavefronts):
+// Kernels: mfa_fwd16_kernel (bf16/fp16, 4 wavefronts; its EXACT
+// instantiation serves single query rows with two-term probabilities),
+// mfa_fwd16_pp_kernel (bf16/fp16, 8 wavefronts on a ping-pong schedule: the
+// two wavefronts of a SIMD alternate MFMA and softmax phases),
+// mfa_fwd16_tk_kernel (at most 32 keys per sequence), mfa_fwd32_kernel
+// (fp32) and mfa_combine_kernel (split-KV merge).  Grouped-query calls pack
+// the query heads of one K/V head into a tile (each wavefront still holds
+// 32 aligned positions of one head).  Shared design:
 //  * The score tile is computed TRANSPOSED, S^T = K * Q^T, with
 //    v_mfma_f32_32x32x16_{bf16,f16} (fp32 inputs: v_mfma_f32_32x32x2_f32).
 //    In the 32x32 MFMA accumulator layout lane l holds column l%32, so every
@@ -33,9 +40,10 @@
 //    every row's exact max, so probabilities stay <= 2 and the row's largest
 //    weight is within one binade of 1.0 when P is rounded to 16 bits.
 //  * Where the number of K/V head groups is a multiple of 8, all tiles of one
-//    K/V head run on one XCD, one (sequence, q head) after another, so its K/V
-//    stays in that XCD's L2; within a head the heaviest tiles (causal: the
-//    last query tiles) go first.
+//    K/V head run on one XCD, so its K/V stays in that XCD's L2: one
+//    (sequence, q head) after another when tiles cost the same, heaviest
+//    tiles of every unit first under causal masks and windows (head-packed
+//    varlen tiles keep the unit order, see decode_tile and make_plan).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
