@@ -203,9 +203,10 @@ __device__ __forceinline__ bool decode_tile(const KArgs& a, int bid, int& b, int
         // and all their tiles.  Within an XCD the order is unit-major (all
         // tiles of one (sequence, q head), heaviest first, then the next), so
         // the workgroups resident on the XCD share one head's K/V in its L2,
-        // when every tile costs the same; when tiles differ (causal, windows)
-        // it is tile-major (the heaviest tiles of every unit first), so the
-        // XCD's CUs take the work longest first and finish together.
+        // or, with a.tile_major (the plan sets it for causal and windowed
+        // calls, except head-packed varlen ones), tile-major: the heaviest
+        // tiles of every unit first, so the XCD's CUs take the work longest
+        // first and finish together.
         const int xcd = bid & ((1 << a.xcd_shift) - 1);
         const int slot = bid >> a.xcd_shift;
         int j;
