@@ -244,7 +244,7 @@ struct Ops {
 // Soft-cap and ALiBi of one raw score (natural-log units), and the soft-cap
 // derivative factor 1 - tanh^2 (1 without soft-cap).
 template <bool BIAS>
-__device__ __forceinline__ float transform(const KArgs& f, float x, float slope, int dist, float& dcap) {
+__device__ __forceinline__ float transform(const KArgs& f, float x, float slope, float dist, float& dcap) {
     dcap = 1.f;
     if constexpr (BIAS) {
         x *= f.scale;
@@ -254,7 +254,7 @@ __device__ __forceinline__ float transform(const KArgs& f, float x, float slope,
             x = f.softcap * t;
             dcap = 1.f - t * t;
         }
-        if (f.alibi) x = fmaf(-slope, fabsf((float)dist), x);
+        if (f.alibi) x = fmaf(-slope, fabsf(dist), x);
     }
     return x;
 }
@@ -508,6 +508,12 @@ mfa_bwd_dkdv_kernel(BArgs a) {
                 const bool full = qs0 + 32 <= Lq && key_lo(f, qs0 + 31 + dq) <= wk0 && key_hi(f, qs0 + dq, Lk) >= wk0 + 31;
                 auto probs = [&](auto masked_tag) {
                     constexpr bool MASKED = decltype(masked_tag)::value;
+                    // ALiBi distance center - key of register r: this lane's
+                    // base plus the register's row offset, exact in fp32
+                    // below 2^24 (formed in each path: the pin keeps the
+                    // per-register values from being hoisted above the branch)
+                    float dist0 = (float)(qs0 + 4 * half + dq - key);
+                    asm volatile("" : "+v"(dist0));
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const float4 l4 = *reinterpret_cast<const float4*>(lse_s[buf] + 32 * sb + 8 * g + 4 * half);
@@ -522,7 +528,7 @@ mfa_bwd_dkdv_kernel(BArgs a) {
                             const int q = qs0 + acc_row(r) + 4 * half;
                             const int center = q + dq;
                             float dcap;
-                            const float x = transform<BIAS>(f, sacc[sb][r], slope, center - key, dcap);
+                            const float x = transform<BIAS>(f, sacc[sb][r], slope, dist0 + (float)acc_row(r), dcap);
                             // (bitwise tests and an unconditional exp: selects, no branches)
                             const float pe = fast_exp2(fmaf(x, c, -lv[i]));
                             bool ok = true;
@@ -806,6 +812,12 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
         const bool full = qs0 + 32 <= Lq && key_lo(f, qs0 + 31 + dq) <= wk0 && key_hi(f, qs0 + dq, Lk) >= wk0 + 31;
         auto probs = [&](auto masked_tag) {
             constexpr bool MASKED = decltype(masked_tag)::value;
+            // ALiBi distance center - key of register r: this lane's base plus
+            // the register's row offset, exact in fp32 below 2^24 (formed in
+            // each path: the pin keeps the per-register values from being
+            // hoisted above the branch)
+            float dist0 = (float)(qs0 + 4 * half + dq - key);
+            asm volatile("" : "+v"(dist0));
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const float4 l4 = *reinterpret_cast<const float4*>(lsb + 8 * g + 4 * half);
@@ -817,7 +829,7 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
                     const int q = qs0 + acc_row(r) + 4 * half;
                     const int center = q + dq;
                     float dcap;
-                    const float x = transform<BIAS>(f, sacc[r], slope, center - key, dcap);
+                    const float x = transform<BIAS>(f, sacc[r], slope, dist0 + (float)acc_row(r), dcap);
                     const float pe = fast_exp2(fmaf(x, c, -lv[i]));
                     bool ok = true;
                     if constexpr (MASKED)
@@ -1106,6 +1118,12 @@ mfa_bwd_dq_kernel(BArgs a) {
             uint32_t dw[8];
             auto dsrow = [&](auto masked_tag) {
                 constexpr bool MASKED = decltype(masked_tag)::value;
+                // ALiBi distance center - key of register r: this lane's base
+                // minus the register's key offset, exact in fp32 below 2^24
+                // (formed in each path: the pin keeps the compiler from
+                // hoisting the 16 per-register values above the branch)
+                float dist0 = (float)(center - kk0 - 4 * half);
+                asm volatile("" : "+v"(dist0));
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
                     float ds2[2];
@@ -1113,7 +1131,7 @@ mfa_bwd_dq_kernel(BArgs a) {
                     for (int i = 0; i < 2; ++i) {
                         const int key = kk0 + acc_row(r + i) + 4 * half;
                         float dcap;
-                        const float x = transform<BIAS>(f, sacc[r + i], slope, center - key, dcap);
+                        const float x = transform<BIAS>(f, sacc[r + i], slope, dist0 - (float)acc_row(r + i), dcap);
                         const float pe = fast_exp2(fmaf(x, c, -lse2));
                         bool ok = true;
                         if constexpr (MASKED) ok = (key >= lo) & (key <= hi) & qin;
