@@ -247,10 +247,13 @@ template <bool BIAS>
 __device__ __forceinline__ float transform(const KArgs& f, float x, float slope, float dist, float& dcap) {
     dcap = 1.f;
     if constexpr (BIAS) {
-        x *= f.scale;
-        if (f.softcap > 0.f) {
-            // tanh(x / cap) = 1 - 2 / (exp(2x/cap) + 1)
-            const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(fast_exp2(x * f.softcap_k) + 1.f);
+        // one multiply: by the scale, or under soft-cap straight by the
+        // exponent's constant (the scale folded in, as in the forward):
+        // tanh(scale*x / cap) = 1 - 2 / (exp2(x * softcap_sk) + 1)
+        const bool cap = f.softcap > 0.f;
+        x *= cap ? f.softcap_sk : f.scale;
+        if (cap) {
+            const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(fast_exp2(x) + 1.f);
             x = f.softcap * t;
             dcap = 1.f - t * t;
         }
