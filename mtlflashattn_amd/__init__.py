@@ -209,12 +209,10 @@ def _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_s
         if page == 0 or page % 256 != 0:
             raise ValueError(f"mtlflashattn_amd: page_block_size {page} must be a positive multiple of 256")
 
-    # One host read of both prefix sums (the reference reads them for the same
-    # checks, metal_flash_attn/__init__.py:145-154); it also yields the true
+    # The prefix sums on the host (the reference reads them for the same
+    # checks, metal_flash_attn/__init__.py:145-154); they also yield the true
     # longest lengths, so a too-small max_seqlen_* cannot drop rows.
-    n = cu_seqlens_q.shape[0]
-    cu = torch.cat([cu_seqlens_q.reshape(-1).to(torch.int64), cu_seqlens_k.reshape(-1).to(torch.int64)]).tolist()
-    cu_q, cu_k = cu[:n], cu[n:]
+    cu_q, cu_k = _host_prefix_sums(cu_seqlens_q, cu_seqlens_k)
     if cu_q[-1] != q.shape[0]:
         raise ValueError(f"mtlflashattn_amd: cu_seqlens_q[-1]={cu_q[-1]} != total_q={q.shape[0]}")
     if not paged and cu_k[-1] != k.shape[0]:
@@ -232,6 +230,36 @@ def _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_s
         scale=scale, causal=causal, softcap=softcap, window_left=window_size[0],
         window_right=window_size[1], alibi_slopes=alibi_slopes, return_lse=return_lse, block_table=block_table,
     )
+
+
+# Host copies of the last varlen call's prefix sums, with the two tensors
+# they were read from and their version counters.  Reading them is a
+# device-to-host copy that waits for all queued GPU work, so a loop of calls
+# on the same cu_seqlens would leave the GPU idle between calls; the copy is
+# reused while the same tensor objects come back with unchanged versions
+# (PyTorch moves a tensor's version on every in-place write through it or
+# through a view of it).  Writes that bypass the counter (through `.data`,
+# or by another library through the raw pointer) are not seen: such a
+# tensor must not be passed again.
+_cu_host = None
+
+
+def _host_prefix_sums(cu_seqlens_q, cu_seqlens_k):
+    global _cu_host
+    cached = _cu_host
+    try:
+        versions = (cu_seqlens_q._version, cu_seqlens_k._version)
+    except RuntimeError:  # inference-mode tensors keep no version counter
+        versions = None
+    if (versions is not None and cached is not None and cached[0] is cu_seqlens_q and cached[1] is cu_seqlens_k
+            and cached[2] == versions):
+        return cached[3], cached[4]
+    n = cu_seqlens_q.shape[0]
+    cu = torch.cat([cu_seqlens_q.reshape(-1).to(torch.int64), cu_seqlens_k.reshape(-1).to(torch.int64)]).tolist()
+    cu_q, cu_k = cu[:n], cu[n:]
+    if versions is not None:
+        _cu_host = (cu_seqlens_q, cu_seqlens_k, versions, cu_q, cu_k)
+    return cu_q, cu_k
 
 
 def _check_block_table(block_table, lens_k, page, num_pages):

@@ -238,6 +238,29 @@ class TestVarlenContract:
             mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6, alibi_slopes=torch.ones(3, 4))
         assert not fake_device
 
+    def test_prefix_sums_read_once_per_tensor_version(self, fake_device, monkeypatch):
+        # repeated calls on the same cu_seqlens read them on the host once; an
+        # in-place write (a new version) or other tensors are read again
+        q, k, v, cu_q, cu_k = self.make()
+        reads = []
+        real_cat = torch.cat
+        monkeypatch.setattr(torch, "cat", lambda ts, *a, **kw: (reads.append(1), real_cat(ts, *a, **kw))[1])
+        mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6)
+        mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6, causal=True)
+        assert len(reads) == 1 and len(fake_device) == 2
+        with pytest.raises(ValueError):  # the cached sums are checked against each call's totals
+            mfa.flash_attn_varlen_func(q[:-1], k, v, cu_q, cu_k, 7, 6)
+        assert len(reads) == 1
+        cu_q[1] = 13  # non-monotonic now: the new version is read and rejected
+        with pytest.raises(ValueError):
+            mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6)
+        assert len(reads) == 2
+        cu_q[1] = 4  # lengths (4, 8): the true longest query length follows the write
+        mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 7, 6)
+        assert len(reads) == 3 and fake_device[-1]["seqlen_q"] == 8
+        mfa.flash_attn_varlen_func(q, k, v, cu_q.clone(), cu_k, 7, 6)  # another tensor
+        assert len(reads) == 4
+
     def test_one_launch_with_true_max_lengths(self, fake_device):
         q, k, v, cu_q, cu_k = self.make(lens_q=(5, 0, 7), lens_k=(6, 4, 3))
         slopes = torch.rand(3, 4)
