@@ -420,10 +420,17 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         soff[i] = (MFA_BWD_PERM ? prow(row) : row) * QST + col;
     }
     float lreg = INFINITY, dreg = 0.f;
-    auto gload = [&](int step) {
-        const int rr = step / nqb;
-        const int q0 = qb0 + (step - rr * nqb) * BQ;
-        const QView qv = q_view(a, b, hq0 + rr);
+    // step order: query head rr (of the R), then its query blocks qi; the
+    // load runs one step ahead of the compute, each with a cursor of its own
+    // (no per-step division)
+    int l_rr = 0, l_qi = 0;
+    auto gload = [&]() {
+        const int q0 = qb0 + l_qi * BQ;
+        const QView qv = q_view(a, b, hq0 + l_rr);
+        if (++l_qi == nqb) {
+            l_qi = 0;
+            ++l_rr;
+        }
         const int rm1 = min(Lq - q0, BQ) - 1;  // q0 < Lq
         const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(qv.q + (int64_t)q0 * f.qs * 2), (short)0, (int)(((int64_t)rm1 * f.qs + D) * 2), kBufferDword3);
@@ -455,16 +462,20 @@ mfa_bwd_dkdv_kernel(BArgs a) {
         }
     };
     if (nsteps > 0) {
-        gload(0);
+        gload();
         swrite(0);
     }
     __syncthreads();
+    int rr = 0, qi = 0;  // the step computed
     for (int step = 0; step < nsteps; ++step) {
         const int buf = step & 1;
-        if (step + 1 < nsteps) gload(step + 1);  // in flight during this step's MFMAs
-        const int rr = step / nqb;
-        const int q0 = qb0 + (step - rr * nqb) * BQ;
+        if (step + 1 < nsteps) gload();  // in flight during this step's MFMAs
+        const int q0 = qb0 + qi * BQ;
         const int hq = hq0 + rr;
+        if (++qi == nqb) {
+            qi = 0;
+            ++rr;
+        }
         const float slope = BIAS && f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
         {
             const uint16_t* qsb = q_s[buf];
