@@ -109,8 +109,11 @@ def test_head_dims(d):
     check_grads(got, ref, torch.bfloat16, f"D={d}", factor=2.0)
 
 
-def test_deterministic():
-    q, k, v = make_qkv(2, 257, 300, 4, 2, 64, torch.bfloat16, seed=9)
+@pytest.mark.parametrize("hq,hkv,D", [(4, 2, 64), (8, 2, 128), (16, 2, 128)])
+def test_deterministic(hq, hkv, D):
+    # D=128: the eight-wavefront dK/dV kernel; 16 query heads per 2 K/V heads
+    # at this size also take the head-group partials and their summing kernel
+    q, k, v = make_qkv(2, 257, 300, hq, hkv, D, torch.bfloat16, seed=9)
     dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(9)).to(DEV, torch.bfloat16)
     f = lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True)  # noqa: E731
     a = grads_of(f, q, k, v, dout)
