@@ -12,7 +12,7 @@ import mtlflashattn_amd as mfa
 from mtlflashattn_amd import _hip, _kernel
 from oracle import chunked
 from gpu_util import (
-    assert_output, assert_parity, default_scale, make_qkv, make_varlen, max_err, native_library_mapped,
+    DEV, assert_output, assert_parity, default_scale, make_qkv, make_varlen, max_err, native_library_mapped,
 )
 
 pytestmark = pytest.mark.gpu
@@ -221,6 +221,24 @@ class TestVarlen:
     def test_ragged_batch(self, dtype):
         self.check_varlen([37, 128, 5], [37, 128, 5], dtype=dtype)
         self.check_varlen([64, 17], [64, 17], dtype=dtype, causal=True)
+
+    def test_prefix_sums_rewritten_in_place(self):
+        # the host copy of cu_seqlens is reused only while the tensors keep
+        # their version: rewriting them in place on the device (same totals,
+        # other lengths) must give the call on fresh tensors, bit for bit
+        q, k, v, cu_q, cu_k = make_varlen([100, 28], [100, 28], 4, 2, 64, torch.bfloat16, seed=41)
+        first = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 100, 100, causal=True)
+        again = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 100, 100, causal=True)
+        assert torch.equal(first, again)
+        cu = torch.tensor([0, 20, 128], dtype=torch.int32, device=DEV)
+        cu_q.copy_(cu)
+        cu_k.copy_(cu)
+        moved = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 108, 108, causal=True)
+        fresh = mfa.flash_attn_varlen_func(q, k, v, cu.clone(), cu.clone(), 108, 108, causal=True)
+        assert torch.equal(moved, fresh)
+        assert not torch.equal(moved, first)
+        ref = chunked.flash_attn_varlen_func(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), causal=True)
+        assert_output(moved, ref, torch.bfloat16, "rewritten cu_seqlens")
 
     def test_ragged_cross_lens(self):
         self.check_varlen([16, 33], [80, 7])
