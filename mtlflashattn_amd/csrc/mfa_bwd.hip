@@ -653,19 +653,28 @@ __global__ void __launch_bounds__(kB8Threads) mfa_bwd_dkdv8_kernel(BArgs a) {
     const int k1 = min(k0 + 128, Lk) - 1;
 
     // K and V rows of the workgroup into LDS (rows past the sequence and
-    // columns past the head dim as zeros)
+    // columns past the head dim as zeros); every chunk of this thread is
+    // loaded before any is stored, one memory round trip for all of them
+    {
+        u32x4_t kk[KCH], vv[KCH];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-        const int cc = tid + NT * i;
-        if (KCH * NT == 128 * CPR || cc < 128 * CPR) {
+        for (int i = 0; i < KCH; ++i) {
+            const int cc = tid + NT * i;
             const int row = cc / CPR, col = (cc % CPR) * 8;
-            u32x4_t kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-            if (k0 + row < Lk && col < D) {
-                kk = *reinterpret_cast<const u32x4_t*>(kv.k + ((int64_t)(k0 + row) * f.ks + col) * 2);
-                vv = *reinterpret_cast<const u32x4_t*>(kv.v + ((int64_t)(k0 + row) * f.vs + col) * 2);
+            kk[i] = vv[i] = u32x4_t{0, 0, 0, 0};
+            if (cc < 128 * CPR && k0 + row < Lk && col < D) {
+                kk[i] = *reinterpret_cast<const u32x4_t*>(kv.k + ((int64_t)(k0 + row) * f.ks + col) * 2);
+                vv[i] = *reinterpret_cast<const u32x4_t*>(kv.v + ((int64_t)(k0 + row) * f.vs + col) * 2);
             }
-            *reinterpret_cast<u32x4_t*>(kv_s + row * ST + col) = kk;
-            *reinterpret_cast<u32x4_t*>(kv_s + (128 + row) * ST + col) = vv;
+        }
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int cc = tid + NT * i;
+            if (KCH * NT == 128 * CPR || cc < 128 * CPR) {
+                const int row = cc / CPR, col = (cc % CPR) * 8;
+                *reinterpret_cast<u32x4_t*>(kv_s + row * ST + col) = kk[i];
+                *reinterpret_cast<u32x4_t*>(kv_s + (128 + row) * ST + col) = vv[i];
+            }
         }
     }
     f32x16_t dka[DB], dva[DB];
