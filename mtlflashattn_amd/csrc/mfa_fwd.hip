@@ -1255,11 +1255,17 @@ mfa_fwd16_kernel(KArgs a) {
 // chunks of each row XOR-swizzled, so the K operand reads (one row per lane)
 // and the transposed V reads (four rows per 16 lanes) are free of bank
 // conflicts.
+// steps of one MFMA phase of the ping-pong kernel
+constexpr int kBothHalves = 0, kQkOnly = 1, kPvOnly = 2;
+
 template <int DP, int QB, int NKB, bool IS_BF16, bool BIAS, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4)))
 mfa_fwd16_pp_kernel(KArgs a) {
     static_assert(NW == 8 || NW == 16, "two or four wavefronts per SIMD");
     constexpr bool SUM_IN_A = MFA_PP_SUM_IN_A;
+    // the first and last MFMA phases run their real half only (head dim 128:
+    // config 4 -1.5 %, config 3 -0.7 %; at 64 the code grew slower by 0.4 %)
+    constexpr bool TRIM = DP > 64;
     constexpr int NT = NW * 64;        // threads
     constexpr int BM = NW * QB * 32;   // query rows per workgroup
     constexpr int BN = NKB * 32;       // keys per K/V block
@@ -1498,11 +1504,15 @@ mfa_fwd16_pp_kernel(KArgs a) {
     // A(u): PV(u-1) then QK(u).  Step i reads one K or V
     // fragment, which feeds both query blocks; fragments are read
     // MFA_PP_AHEAD steps ahead of their MFMAs (sched_barrier keeps the
-    // compiler from hoisting every read to the top).
-    auto phase_a = [&](int u) __attribute__((always_inline)) {
+    // compiler from hoisting every read to the top).  PART selects the
+    // steps: both halves, the QK half only (A(0): block -1 has no P) or the
+    // PV half only (A(n): block n has no scores to compute).
+    auto phase_a = [&](int u, auto part_c) __attribute__((always_inline)) {
+        constexpr int PART = decltype(part_c)::value;
         constexpr int NPV = DB * NKB * 2;
         constexpr int NQK = NKB * DS;
-        constexpr int NS = NPV + NQK;
+        constexpr int I0 = PART == kQkOnly ? NPV : 0;         // first step
+        constexpr int NS = PART == kPvOnly ? NPV : NPV + NQK;  // end of the steps
         constexpr int AH = NW == 16 ? MFA_PP_AHEAD16 : QB == 1 ? (DP > 64 ? MFA_PP_AHEAD1W : MFA_PP_AHEAD1) : MFA_PP_AHEAD;
         const uint16_t* vt = vst0 + ((u + NST - 1) % NST) * TILE;
         const uint16_t* kt = kst0 + (u % NST) * TILE;
@@ -1520,7 +1530,8 @@ mfa_fwd16_pp_kernel(KArgs a) {
         op_t kfr[AH + 1];
         auto load_step = [&](auto ic) __attribute__((always_inline)) {
             constexpr int i = decltype(ic)::value;
-            if constexpr (i < NPV) {
+            if constexpr (i < I0) {
+            } else if constexpr (i < NPV) {
                 constexpr int db = i % DB, ks = i / DB, kb = ks / 2, st = ks % 2;
                 constexpr int off = (32 * kb + 16 * st) * DP * 2;
                 vlo[i % (AH + 1)] = lds_read_tr16<off>(vp[db]);
@@ -1556,8 +1567,10 @@ mfa_fwd16_pp_kernel(KArgs a) {
             }
         };
         if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(MFA_PP_PRIO);
-        static_for<AH>(load_step);
-        if constexpr (SUM_IN_A) {
+        static_for<AH>([&](auto ic) __attribute__((always_inline)) {
+            load_step(std::integral_constant<int, I0 + decltype(ic)::value>{});
+        });
+        if constexpr (SUM_IN_A && PART != kQkOnly) {
             // row sums of P(u-1), whose rescale (if any) B(u-1) applied to l
             // (the pins keep the compiler from moving the sums into B)
 #pragma unroll
@@ -1572,10 +1585,10 @@ mfa_fwd16_pp_kernel(KArgs a) {
             for (int qb = 0; qb < QB; ++qb) pin(rs[qb].l);
         }
         __builtin_amdgcn_sched_barrier(0);
-        static_for<NS>([&](auto ic) __attribute__((always_inline)) {
-            constexpr int i = decltype(ic)::value;
+        static_for<NS - I0>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = I0 + decltype(ic)::value;
             load_step(std::integral_constant<int, i + AH>{});
-            mfma_step(ic);
+            mfma_step(std::integral_constant<int, i>{});
             __builtin_amdgcn_sched_barrier(0);
         });
         if constexpr (MFA_PP_PRIO) __builtin_amdgcn_s_setprio(0);
@@ -1646,17 +1659,20 @@ mfa_fwd16_pp_kernel(KArgs a) {
 #pragma unroll
                 for (int st = 0; st < 2; ++st) pin(pw[qb][kb][st]);
     };
-    // ---- prologue: K(0), K(1), V(0) resident.  A(0) runs PV(-1) with P = 0
-    // against the zeroed V stage of block -1; A(n) runs a QK of block n whose
-    // result is never used.  (One instance of each phase.)
-    for (int c2 = tid; c2 < TILE / 8; c2 += NT)
-        *reinterpret_cast<u32x4_t*>(vst0 + (NST - 1) * TILE + 8 * c2) = u32x4_t{0, 0, 0, 0};
+    // ---- prologue: K(0), K(1), V(0) resident.  With TRIM, A(0) runs only
+    // the QK of block 0 and A(n) only the PV of block n-1; without, A(0) runs
+    // PV(-1) with P = 0 against the zeroed V stage of block -1 and A(n) a QK
+    // of block n whose result is never used.
+    if constexpr (!TRIM) {
+        for (int c2 = tid; c2 < TILE / 8; c2 += NT)
+            *reinterpret_cast<u32x4_t*>(vst0 + (NST - 1) * TILE + 8 * c2) = u32x4_t{0, 0, 0, 0};
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int st = 0; st < 2; ++st) pw[qb][kb][st] = u32x4_t{0, 0, 0, 0};
+                for (int st = 0; st < 2; ++st) pw[qb][kb][st] = u32x4_t{0, 0, 0, 0};
+    }
     load_k(0);
     load_k(1);
     load_v(0);
@@ -1685,17 +1701,23 @@ mfa_fwd16_pp_kernel(KArgs a) {
             if constexpr (!LATE) dma(0);
             phase_sync(std::integral_constant<bool, !LATE>{});  // phase 0 (idle)
         }
-        for (int u = 0; u < nblk; ++u) {
+        auto step = [&](int u, auto part_c) __attribute__((always_inline)) {
             if constexpr (G == 0 || LATE) dma(u);
-            phase_a(u);
+            phase_a(u, part_c);
             if constexpr (G == 0) phase_sync(EVEN{}); else phase_sync(ODD{});
             if constexpr (G == 1 && !LATE) dma(u + 1);
             phase_b(u);
             if constexpr (G == 0) phase_sync(ODD{});
             else phase_sync(std::integral_constant<bool, !LATE>{});
+        };
+        if constexpr (TRIM) {
+            step(0, std::integral_constant<int, kQkOnly>{});  // (nblk >= 1 here)
+            for (int u = 1; u < nblk; ++u) step(u, std::integral_constant<int, kBothHalves>{});
+        } else {
+            for (int u = 0; u < nblk; ++u) step(u, std::integral_constant<int, kBothHalves>{});
         }
         if constexpr (G == 0 || LATE) dma(nblk);
-        phase_a(nblk);
+        phase_a(nblk, std::integral_constant<int, TRIM ? kPvOnly : kBothHalves>{});
         if constexpr (G == 0) {
             phase_sync(EVEN{});  // phase 2n
             phase_sync(ODD{});   // phase 2n+1 (idle)
