@@ -125,6 +125,15 @@ class TestFlashAttnFunc:
         check(q, k, v, f"D={d} causal", causal=True)
 
     @pytest.mark.parametrize("dtype", DTYPES)
+    def test_single_key_block(self, dtype):
+        # every tile walks one 64-key block, so its first MFMA phase is also
+        # its last (head dim 128 ping-pong tiles: a QK-only phase, then a
+        # PV-only one)
+        for lq, lk, causal in ((300, 40, False), (64, 64, True), (200, 64, True), (1000, 17, False)):
+            q, k, v = make_qkv(1, lq, lk, 2, 2, 128, dtype, seed=lq)
+            check(q, k, v, f"Lq={lq} Lk={lk} causal={causal}", causal=causal)
+
+    @pytest.mark.parametrize("dtype", DTYPES)
     def test_custom_softmax_scale(self, dtype):
         q, k, v = make_qkv(1, 64, 64, 2, 2, 64, dtype)
         check(q, k, v, softmax_scale=0.25)
