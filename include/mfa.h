@@ -261,6 +261,10 @@ int mfa_fwd_splitkv_static(const mfa_fwd_params* params, int32_t split_keys, voi
  * With grouped-query heads, dK/dV of a K/V head sum over its query heads.
  * Deterministic (no atomics): one kernel owns each dK/dV block and loops over
  * every query of its K/V head; another owns each dQ block.
+ * fp32 (dtype_in = MFA_DTYPE_F32: q, k, v, o, dout and the gradients fp32)
+ * runs fp32 kernels on the vector ALU with the fp32 forward's score transform
+ * (strides then multiples of 4 elements; the workspace holds the row sums
+ * only).  bf16/fp16 run on the matrix cores.
  */
 typedef struct mfa_bwd_params {
     /* q, k, v, o (the forward output), shapes, strides, masks and biases as
@@ -284,7 +288,7 @@ typedef struct mfa_bwd_params {
     const float* dlse;
 } mfa_bwd_params;
 
-/* 1 if mfa_bwd implements (dtype_in, head_dim): bf16/fp16, head_dim a
+/* 1 if mfa_bwd implements (dtype_in, head_dim): bf16/fp16/fp32, head_dim a
  * multiple of 8 up to MFA_MAX_HEAD_DIM. */
 int mfa_bwd_supported(int32_t dtype_in, int32_t head_dim);
 /* Device workspace mfa_bwd needs, 0 for an empty problem, < 0 on error: the

@@ -6,10 +6,11 @@ raise NotImplementedError so callers can fall back, rather than silently
 approximating (metal_flash_attn/__init__.py:1-5).
 
 Backward: the reference is inference-only (metal_flash_attn/__init__.py:3-4).
-Here bf16/fp16 calls whose inputs require grad are differentiable through
-HIP backward kernels (dq, dk, dv; the returned lse too).  fp32 inputs and
-paged K/V stay forward-only: their backward raises NotImplementedError, as
-do dropout_p > 0, deterministic=True and return_attn_probs=True.
+Here calls whose inputs require grad are differentiable through HIP
+backward kernels (dq, dk, dv; the returned lse too): bf16/fp16 on the matrix
+cores, fp32 in fp32 on the vector ALU.  Paged K/V stay forward-only: their
+backward raises NotImplementedError, as do dropout_p > 0, deterministic=True
+and return_attn_probs=True.
 
 Two additions the reference raises for: `flash_attn_varlen_func` accepts a
 paged K/V cache (`block_table`, CUDA flash-attn's layout), and

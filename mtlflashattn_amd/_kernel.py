@@ -510,8 +510,6 @@ def _run_bwd(q, k, v, out, dout, lse, *, scale, causal, softcap, window_left, wi
     the parity mode).
     """
     _kernel_mode()
-    if q.dtype == torch.float32:
-        raise NotImplementedError("mtlflashattn_amd: the backward takes bf16/fp16 inputs (no fp32 HIP backward)")
     _check_device(q, k, v, out, dout)
     B, Sq, Hq, D = q.shape
     Hkv = k.shape[2]

@@ -29,6 +29,8 @@
 //    lane = query, and dQ^T += K^T dS^T takes dS^T from the accumulators.
 // Tiles whose query-key pairs are all valid skip the masks; boundary tiles
 // mask element-wise with selects (no branches).
+// fp32 inputs run mfa_bwd32_* kernels: the same decomposition with fp32
+// products on the vector ALU (see their section below).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -1202,6 +1204,380 @@ mfa_bwd_dq_kernel(BArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// fp32 backward: fp32 q, k, v, o and dO in, fp32 dq, dk and dv out.  The same
+// decomposition as the 16-bit kernels (Dsum; dK/dV for a block of keys of one
+// (sequence, K/V head), walking every query block of its head group that
+// sees them; dQ for a block of query rows, walking the key blocks they see),
+// with fp32 products on the vector ALU over LDS tiles and the fp32 forward's
+// score transform (precise tanh under soft-cap): the gradients of an fp32
+// forward, computed in fp32 end to end.  Tiles: 32 query rows x 64 keys;
+// thread t computes the scores of rows 2*(t/16), +1 and keys 4*(t%16)..+3.
+
+constexpr int kB32Rows = 32;              // query rows of a tile
+constexpr int kB32Keys = 64;              // keys of a tile
+constexpr int kB32KT = kB32Keys + 4;      // row stride (floats) of transposed K/V tiles
+
+// Per (sequence, query head) / (sequence, K/V head) rows of fp32 tensors
+// (element offsets, as q_view / k_view).
+struct QView32 {
+    const float* q;
+    const float* dout;
+    const float* o;
+    float* dq;
+    const float* lse;
+    float* dsum;
+    int Lq, Lk;
+};
+__device__ __forceinline__ QView32 q_view32(const BArgs& a, int b, int hq) {
+    const KArgs& f = a.f;
+    QView32 s;
+    int64_t qs = 0, qb = 0;
+    if (f.cu_q) {
+        const int q0 = f.cu_q[b];
+        s.Lq = f.cu_q[b + 1] - q0;
+        s.Lk = f.cu_k[b + 1] - f.cu_k[b];
+        qs = q0;
+        s.lse = f.lse + (int64_t)hq * f.lse_h + q0;
+    } else {
+        s.Lq = f.Lq;
+        s.Lk = f.Lk;
+        qb = b;
+        s.lse = f.lse + (int64_t)b * f.lse_b + (int64_t)hq * f.lse_h;
+    }
+    s.q = reinterpret_cast<const float*>(f.q) + (qb * f.qb + qs * f.qs + (int64_t)hq * f.qh);
+    s.o = reinterpret_cast<const float*>(f.o) + (qb * f.ob + qs * f.os + (int64_t)hq * f.oh);
+    s.dout = reinterpret_cast<const float*>(a.dout) + (qb * a.dob + qs * a.dos + (int64_t)hq * a.doh);
+    s.dq = reinterpret_cast<float*>(a.dq) + (qb * a.dqb + qs * a.dqs + (int64_t)hq * a.dqh);
+    s.dsum = a.dsum + ((int64_t)b * f.Hq + hq) * f.Lq;
+    return s;
+}
+struct KView32 {
+    const float* k;
+    const float* v;
+    float* dk;
+    float* dv;
+    int Lk;
+};
+__device__ __forceinline__ KView32 k_view32(const BArgs& a, int b, int hkv) {
+    const KArgs& f = a.f;
+    KView32 s;
+    int64_t ks = 0, kb = 0;
+    if (f.cu_k) {
+        ks = f.cu_k[b];
+        s.Lk = f.cu_k[b + 1] - f.cu_k[b];
+    } else {
+        kb = b;
+        s.Lk = f.Lk;
+    }
+    s.k = reinterpret_cast<const float*>(f.k) + (kb * f.kb + ks * f.ks + (int64_t)hkv * f.kh);
+    s.v = reinterpret_cast<const float*>(f.v) + (kb * f.vb + ks * f.vs + (int64_t)hkv * f.vh);
+    s.dk = reinterpret_cast<float*>(a.dk) + (kb * a.dkb + ks * a.dks + (int64_t)hkv * a.dkh);
+    s.dv = reinterpret_cast<float*>(a.dv) + (kb * a.dvb + ks * a.dvs + (int64_t)hkv * a.dvh);
+    return s;
+}
+
+// Rows [0, NROWS) of an fp32 [rows, D] tile (row stride `st` floats) into
+// LDS, transposed (t[d * TS + row]) and, with ROWS, also row-major
+// (r[row * (DP + 4) + d]).  Rows >= `valid` and columns >= D read as 0.
+// Every load of a thread is issued before its LDS stores.
+template <int DP, int NROWS, int TS, bool ROWS>
+__device__ __forceinline__ void stage32(const float* src, int64_t st, int valid, int D, float* t, float* r, int tid) {
+    constexpr int C4 = DP / 4;  // float4 chunks per row
+    constexpr int N = (NROWS * C4 + kBThreads - 1) / kBThreads;
+    float4 v[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int cc = tid + kBThreads * i;
+        const int row = cc / C4, col = (cc % C4) * 4;
+        v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (cc < NROWS * C4 && row < valid && col < D)
+            v[i] = *reinterpret_cast<const float4*>(src + (int64_t)row * st + col);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int cc = tid + kBThreads * i;
+        if (N * kBThreads == NROWS * C4 || cc < NROWS * C4) {
+            const int row = cc / C4, col = (cc % C4) * 4;
+            t[(col + 0) * TS + row] = v[i].x;
+            t[(col + 1) * TS + row] = v[i].y;
+            t[(col + 2) * TS + row] = v[i].z;
+            t[(col + 3) * TS + row] = v[i].w;
+            if constexpr (ROWS) *reinterpret_cast<float4*>(r + row * (DP + 4) + col) = v[i];
+        }
+    }
+}
+
+// S = Q K^T and dP = dO V^T of one 32 x 64 tile from transposed LDS tiles
+// (q / dO: [DP][32], k / v: [DP][kB32KT]): rows r, r+1, keys c..c+3.
+template <int DP>
+__device__ __forceinline__ void tile_products32(const float* qt, const float* dot, const float* kt, const float* vt,
+                                                int r, int c, float (&s)[2][4], float (&g)[2][4]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[i][j] = g[i][j] = 0.f;
+#pragma unroll 4
+    for (int d = 0; d < DP; ++d) {
+        const float2 qa = *reinterpret_cast<const float2*>(qt + d * kB32Rows + r);
+        const float2 ga = *reinterpret_cast<const float2*>(dot + d * kB32Rows + r);
+        const float4 kb = *reinterpret_cast<const float4*>(kt + d * kB32KT + c);
+        const float4 vb = *reinterpret_cast<const float4*>(vt + d * kB32KT + c);
+        const float kk[4] = {kb.x, kb.y, kb.z, kb.w}, vv[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s[0][j] = fmaf(qa.x, kk[j], s[0][j]);
+            s[1][j] = fmaf(qa.y, kk[j], s[1][j]);
+            g[0][j] = fmaf(ga.x, vv[j], g[0][j]);
+            g[1][j] = fmaf(ga.y, vv[j], g[1][j]);
+        }
+    }
+}
+
+// One query row's data for the tile: exp2-domain lse, Dsum, center and
+// valid key interval (hi = -1 for a row past the sequence).
+struct Row32 {
+    float lse2, dsum;
+    int center, lo, hi;
+};
+__device__ __forceinline__ Row32 row32(const KArgs& f, const QView32& qv, int q, int dq, int Lk) {
+    Row32 w;
+    const bool in = q < qv.Lq;
+    w.lse2 = in ? lse2_of(qv.lse[q]) : INFINITY;
+    w.dsum = in ? qv.dsum[q] : 0.f;
+    w.center = q + dq;
+    w.lo = key_lo(f, w.center);
+    w.hi = in ? key_hi(f, w.center, Lk) : -1;
+    return w;
+}
+
+// P and dS * d score / d (q.k) of one (row, key) pair from s = q.k and dP:
+// score = scale*s, soft-cap (precise tanh), ALiBi; P = exp(score - lse).
+__device__ __forceinline__ void pair32(const KArgs& f, const Row32& w, float slope, int key, float s, float dp,
+                                       float& p, float& ds) {
+    float x = s * f.scale, dx = f.scale;
+    if (f.softcap > 0.f) {
+        const float t = precise_tanh(__fdiv_rn(x, f.softcap));
+        x = f.softcap * t;
+        dx *= 1.f - t * t;
+    }
+    if (f.alibi) x = fmaf(-slope, fabsf((float)(w.center - key)), x);
+    const bool valid = key >= w.lo && key <= w.hi;
+    p = valid ? fast_exp2(fmaf(x, kLog2e, -w.lse2)) : 0.f;
+    ds = p * (dp - w.dsum) * dx;
+}
+
+// Dsum = rowsum(dO * O) - dlse in fp32: 16 lanes per row, 8 elements per lane.
+__global__ void __launch_bounds__(kBThreads) mfa_bwd32_dsum_kernel(BArgs a) {
+    const int bid = blockIdx.x;
+    const int unit = bid / a.T, tile = bid - unit * a.T;
+    const int b = unit / a.f.Hq, hq = unit - b * a.f.Hq;
+    const QView32 qv = q_view32(a, b, hq);
+    const int row = tile * 16 + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+    float acc = 0.f;
+    const int d0 = sub * 8;
+    if (row < qv.Lq && d0 < a.f.D) {  // (D is a multiple of 8)
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+            const float4 o = *reinterpret_cast<const float4*>(qv.o + (int64_t)row * a.f.os + d0 + e);
+            const float4 g = *reinterpret_cast<const float4*>(qv.dout + (int64_t)row * a.dos + d0 + e);
+            acc = fmaf(o.x, g.x, acc);
+            acc = fmaf(o.y, g.y, acc);
+            acc = fmaf(o.z, g.z, acc);
+            acc = fmaf(o.w, g.w, acc);
+        }
+    }
+    acc += __shfl_xor(acc, 8);
+    acc += __shfl_xor(acc, 4);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 1);
+    if (sub == 0 && row < qv.Lq) {
+        if (a.dlse) {
+            const float* dl = a.dlse + (qv.lse - a.f.lse);
+            acc -= dl[row];
+        }
+        qv.dsum[row] = acc;
+    }
+}
+
+// dQ of 32 query rows: dQ = sum over key blocks of dS' K (dS' = dS * d score
+// / d(q.k)), K staged transposed (for S) and row-major (for the product).
+template <int DP>
+__global__ void __launch_bounds__(kBThreads) mfa_bwd32_dq_kernel(BArgs a) {
+    const KArgs& f = a.f;
+    const int unit = blockIdx.x / a.T, tile = blockIdx.x - unit * a.T;
+    const int b = unit / f.Hq, hq = unit - b * f.Hq;
+    const QView32 qv = q_view32(a, b, hq);
+    const KView32 kv = k_view32(a, b, hq / (f.Hq / f.Hkv));
+    const int Lq = qv.Lq, Lk = kv.Lk, D = f.D;
+    const int q0 = tile * kB32Rows;
+    if (q0 >= Lq) return;
+    const int tid = threadIdx.x;
+    const int r = 2 * (tid >> 4), c = 4 * (tid & 15);
+    constexpr int DC = DP / 16;  // dQ columns per thread
+    const int d0 = (tid & 15) * DC;
+    const int dq = Lk - Lq;
+    const int nrow = min(kB32Rows, Lq - q0);
+
+    __shared__ __attribute__((aligned(16))) float qt[DP * kB32Rows];
+    __shared__ __attribute__((aligned(16))) float dot[DP * kB32Rows];
+    __shared__ __attribute__((aligned(16))) float kt[DP * kB32KT];
+    __shared__ __attribute__((aligned(16))) float vt[DP * kB32KT];
+    __shared__ __attribute__((aligned(16))) float kr[kB32Keys * (DP + 4)];
+    __shared__ __attribute__((aligned(16))) float dst[kB32Keys * kB32Rows];  // dS'^T [key][row]
+
+    stage32<DP, kB32Rows, kB32Rows, false>(qv.q + (int64_t)q0 * f.qs, f.qs, nrow, D, qt, nullptr, tid);
+    stage32<DP, kB32Rows, kB32Rows, false>(qv.dout + (int64_t)q0 * a.dos, a.dos, nrow, D, dot, nullptr, tid);
+    const Row32 w0 = row32(f, qv, q0 + r, dq, Lk), w1 = row32(f, qv, q0 + r + 1, dq, Lk);
+    const float slope = f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
+
+    float acc[2][DC];
+#pragma unroll
+    for (int e = 0; e < DC; ++e) acc[0][e] = acc[1][e] = 0.f;
+    // key blocks any row of the tile sees (the bounds are monotone in the row)
+    const int klo = key_lo(f, q0 + dq), khi = key_hi(f, q0 + nrow - 1 + dq, Lk);
+    for (int j0 = (klo / kB32Keys) * kB32Keys; j0 <= khi; j0 += kB32Keys) {
+        const int nk = min(kB32Keys, Lk - j0);
+        __syncthreads();  // (the previous block's LDS reads are done; the Q tiles are visible)
+        stage32<DP, kB32Keys, kB32KT, true>(kv.k + (int64_t)j0 * f.ks, f.ks, nk, D, kt, kr, tid);
+        stage32<DP, kB32Keys, kB32KT, false>(kv.v + (int64_t)j0 * f.vs, f.vs, nk, D, vt, nullptr, tid);
+        __syncthreads();
+        float s[2][4], g[2][4];
+        tile_products32<DP>(qt, dot, kt, vt, r, c, s, g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float p, ds0, ds1;
+            pair32(f, w0, slope, j0 + c + j, s[0][j], g[0][j], p, ds0);
+            pair32(f, w1, slope, j0 + c + j, s[1][j], g[1][j], p, ds1);
+            *reinterpret_cast<float2*>(dst + (c + j) * kB32Rows + r) = make_float2(ds0, ds1);
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int j = 0; j < kB32Keys; ++j) {
+            const float2 gr = *reinterpret_cast<const float2*>(dst + j * kB32Rows + r);
+            const float* kp = kr + j * (DP + 4) + d0;
+#pragma unroll
+            for (int e = 0; e < DC; e += 2) {
+                const float2 kk = *reinterpret_cast<const float2*>(kp + e);
+                acc[0][e] = fmaf(gr.x, kk.x, acc[0][e]);
+                acc[0][e + 1] = fmaf(gr.x, kk.y, acc[0][e + 1]);
+                acc[1][e] = fmaf(gr.y, kk.x, acc[1][e]);
+                acc[1][e + 1] = fmaf(gr.y, kk.y, acc[1][e + 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = q0 + r + i;
+        if (q < Lq) {
+#pragma unroll
+            for (int e = 0; e < DC; ++e)
+                if (d0 + e < D) qv.dq[(int64_t)q * a.dqs + d0 + e] = acc[i][e];
+        }
+    }
+}
+
+// dK and dV of 64 keys of one (sequence, K/V head): every query block of
+// every query head of the group that sees the keys adds P^T dO to dV and
+// dS'^T Q to dK (in a fixed order: the result does not depend on scheduling).
+template <int DP>
+__global__ void __launch_bounds__(kBThreads) mfa_bwd32_dkdv_kernel(BArgs a) {
+    const KArgs& f = a.f;
+    const int ukv = blockIdx.x / a.T, ktile = blockIdx.x - ukv * a.T;
+    const int b = ukv / f.Hkv, hkv = ukv - b * f.Hkv;
+    const KView32 kv = k_view32(a, b, hkv);
+    const int Lk = kv.Lk, D = f.D;
+    const int k0 = ktile * kB32Keys;
+    if (k0 >= Lk) return;
+    const int nk = min(kB32Keys, Lk - k0);
+    const int tid = threadIdx.x;
+    const int r = 2 * (tid >> 4), c = 4 * (tid & 15);  // score tile: rows r, r+1; keys c..c+3
+    constexpr int DC = DP / 16;
+    const int kk0 = 4 * (tid >> 4), d0 = (tid & 15) * DC;  // dK/dV tile: keys kk0..kk0+3, columns d0..
+
+    __shared__ __attribute__((aligned(16))) float kt[DP * kB32KT];
+    __shared__ __attribute__((aligned(16))) float vt[DP * kB32KT];
+    __shared__ __attribute__((aligned(16))) float qt[DP * kB32Rows];
+    __shared__ __attribute__((aligned(16))) float dot[DP * kB32Rows];
+    __shared__ __attribute__((aligned(16))) float qr[kB32Rows * (DP + 4)];
+    __shared__ __attribute__((aligned(16))) float dor[kB32Rows * (DP + 4)];
+    __shared__ __attribute__((aligned(16))) float ps[kB32Rows * kB32Keys];  // P [row][key]
+    __shared__ __attribute__((aligned(16))) float gs[kB32Rows * kB32Keys];  // dS' [row][key]
+
+    stage32<DP, kB32Keys, kB32KT, false>(kv.k + (int64_t)k0 * f.ks, f.ks, nk, D, kt, nullptr, tid);
+    stage32<DP, kB32Keys, kB32KT, false>(kv.v + (int64_t)k0 * f.vs, f.vs, nk, D, vt, nullptr, tid);
+
+    float dk[4][DC], dv[4][DC];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < DC; ++e) dk[j][e] = dv[j][e] = 0.f;
+    const int R = f.Hq / f.Hkv;
+    const int Lq = f.cu_q ? f.cu_q[b + 1] - f.cu_q[b] : f.Lq;
+    const int dq = Lk - Lq;
+    const int k1 = k0 + nk - 1;
+    for (int rr = 0; rr < R; ++rr) {
+        const int hq = hkv * R + rr;
+        const QView32 qv = q_view32(a, b, hq);
+        const float slope = f.alibi ? f.alibi[b * f.alibi_bstride + hq] : 0.f;
+        for (int q0 = 0; q0 < Lq; q0 += kB32Rows) {
+            const int nrow = min(kB32Rows, Lq - q0);
+            // (no row of the block sees a key of the tile: the bounds are monotone in the row)
+            if (key_hi(f, q0 + nrow - 1 + dq, Lk) < k0 || key_lo(f, q0 + dq) > k1) continue;
+            __syncthreads();  // (the previous block's LDS reads are done; the K/V tiles are visible)
+            stage32<DP, kB32Rows, kB32Rows, true>(qv.q + (int64_t)q0 * f.qs, f.qs, nrow, D, qt, qr, tid);
+            stage32<DP, kB32Rows, kB32Rows, true>(qv.dout + (int64_t)q0 * a.dos, a.dos, nrow, D, dot, dor, tid);
+            const Row32 w0 = row32(f, qv, q0 + r, dq, Lk), w1 = row32(f, qv, q0 + r + 1, dq, Lk);
+            __syncthreads();
+            float s[2][4], g[2][4];
+            tile_products32<DP>(qt, dot, kt, vt, r, c, s, g);
+            float p0[4], p1[4], g0[4], g1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pair32(f, w0, slope, k0 + c + j, s[0][j], g[0][j], p0[j], g0[j]);
+                pair32(f, w1, slope, k0 + c + j, s[1][j], g[1][j], p1[j], g1[j]);
+            }
+            *reinterpret_cast<float4*>(ps + r * kB32Keys + c) = make_float4(p0[0], p0[1], p0[2], p0[3]);
+            *reinterpret_cast<float4*>(ps + (r + 1) * kB32Keys + c) = make_float4(p1[0], p1[1], p1[2], p1[3]);
+            *reinterpret_cast<float4*>(gs + r * kB32Keys + c) = make_float4(g0[0], g0[1], g0[2], g0[3]);
+            *reinterpret_cast<float4*>(gs + (r + 1) * kB32Keys + c) = make_float4(g1[0], g1[1], g1[2], g1[3]);
+            __syncthreads();
+#pragma unroll 2
+            for (int i = 0; i < nrow; ++i) {
+                const float4 pv = *reinterpret_cast<const float4*>(ps + i * kB32Keys + kk0);
+                const float4 gv = *reinterpret_cast<const float4*>(gs + i * kB32Keys + kk0);
+                const float pj[4] = {pv.x, pv.y, pv.z, pv.w}, gj[4] = {gv.x, gv.y, gv.z, gv.w};
+                const float* op = dor + i * (DP + 4) + d0;
+                const float* qp = qr + i * (DP + 4) + d0;
+#pragma unroll
+                for (int e = 0; e < DC; e += 2) {
+                    const float2 ov = *reinterpret_cast<const float2*>(op + e);
+                    const float2 qv2 = *reinterpret_cast<const float2*>(qp + e);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        dv[j][e] = fmaf(pj[j], ov.x, dv[j][e]);
+                        dv[j][e + 1] = fmaf(pj[j], ov.y, dv[j][e + 1]);
+                        dk[j][e] = fmaf(gj[j], qv2.x, dk[j][e]);
+                        dk[j][e + 1] = fmaf(gj[j], qv2.y, dk[j][e + 1]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int key = k0 + kk0 + j;
+        if (key < Lk) {
+#pragma unroll
+            for (int e = 0; e < DC; ++e)
+                if (d0 + e < D) {
+                    kv.dk[(int64_t)key * a.dks + d0 + e] = dk[j][e];
+                    kv.dv[(int64_t)key * a.dvs + d0 + e] = dv[j][e];
+                }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // host side
 
 int bset_err(int code, const char* fmt, ...) {
@@ -1217,6 +1593,8 @@ typedef void (*bkernel_fn)(BArgs);
 struct BwdKernels {
     bkernel_fn dsum, dkdv, dq, dkdv_sum;
     int dkdv_threads;
+    int dkdv_keys = 128;  // keys per dK/dV workgroup
+    int dq_rows = 128;    // query rows per dQ workgroup
 };
 
 template <int DP, bool IS_BF16>
@@ -1246,6 +1624,27 @@ BwdKernels bwd_select(int dp, bool bias) {
     }
 }
 
+template <int DP>
+BwdKernels bwd32_kernels() {
+    BwdKernels k;
+    k.dsum = mfa_bwd32_dsum_kernel;
+    k.dkdv = mfa_bwd32_dkdv_kernel<DP>;
+    k.dq = mfa_bwd32_dq_kernel<DP>;
+    k.dkdv_sum = nullptr;  // (one workgroup per K/V head's keys: no partials)
+    k.dkdv_threads = kBThreads;
+    k.dkdv_keys = kB32Keys;
+    k.dq_rows = kB32Rows;
+    return k;
+}
+BwdKernels bwd32_select(int dp) {
+    switch (dp) {
+        case 32: return bwd32_kernels<32>();
+        case 64: return bwd32_kernels<64>();
+        case 96: return bwd32_kernels<96>();
+        default: return bwd32_kernels<128>();
+    }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct BPlan {
@@ -1261,8 +1660,9 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     if (!bp) return bset_err(MFA_ERR_INVALID, "mfa_bwd: params is NULL");
     const mfa_fwd_params* p = &bp->fwd;
     const int din = p->dtype_in;
-    if (din != MFA_DTYPE_F16 && din != MFA_DTYPE_BF16)
-        return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: dtype_in %d (the backward takes bf16/fp16)", din);
+    const bool f32 = din == MFA_DTYPE_F32;
+    if (din != MFA_DTYPE_F16 && din != MFA_DTYPE_BF16 && !f32)
+        return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: dtype_in %d (the backward takes bf16/fp16/fp32)", din);
     if (p->dtype_out != din)
         return bset_err(MFA_ERR_UNSUPPORTED, "mfa_bwd: o and dout must have dtype_in");
     if (bp->dtype_grad != din && bp->dtype_grad != MFA_DTYPE_F32)
@@ -1293,8 +1693,9 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
                                  p->v_head_stride, p->o_batch_stride, p->o_seq_stride, p->o_head_stride,
                                  bp->do_batch_stride, bp->do_seq_stride, bp->do_head_stride};
         for (int i = 0; i < 15; ++i)
-            if (s16[i] % 8 != 0)
-                return bset_err(MFA_ERR_INVALID, "mfa_bwd: q/k/v/o/dout strides must be multiples of 8 elements");
+            if (s16[i] % (f32 ? 4 : 8) != 0)
+                return bset_err(MFA_ERR_INVALID, "mfa_bwd: q/k/v/o/dout strides must be multiples of %d elements",
+                                f32 ? 4 : 8);
         const int64_t sg[9] = {bp->dq_batch_stride, bp->dq_seq_stride, bp->dq_head_stride, bp->dk_batch_stride,
                                bp->dk_seq_stride, bp->dk_head_stride, bp->dv_batch_stride, bp->dv_seq_stride,
                                bp->dv_head_stride};
@@ -1306,14 +1707,15 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
             return bset_err(MFA_ERR_INVALID, "mfa_bwd: lse strides must be >= 0");
         // staged blocks (up to 128 rows: the dK/dV kernel's query steps above
         // head dim 64) are addressed with 32-bit byte offsets
+        // (the fp32 kernels form 64-bit offsets)
         const int64_t rs[4] = {p->q_seq_stride, bp->do_seq_stride, p->k_seq_stride, p->v_seq_stride};
         for (int i = 0; i < 4; ++i)
-            if (rs[i] < 0 || (127 * rs[i] + D) * 2 >= ((int64_t)1 << 31))
+            if (rs[i] < 0 || (!f32 && (127 * rs[i] + D) * 2 >= ((int64_t)1 << 31)))
                 return bset_err(MFA_ERR_INVALID, "mfa_bwd: sequence strides must be >= 0 and span < 2 GiB per 128 rows");
     }
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128;
     const bool bias = p->softcap > 0.f || p->alibi_slopes != nullptr || !(p->scale > 0.f);
-    plan->k = din == MFA_DTYPE_BF16 ? bwd_select<true>(dp, bias) : bwd_select<false>(dp, bias);
+    plan->k = f32 ? bwd32_select(dp) : din == MFA_DTYPE_BF16 ? bwd_select<true>(dp, bias) : bwd_select<false>(dp, bias);
 
     BArgs& a = plan->a;
     memset(&a, 0, sizeof(a));
@@ -1367,7 +1769,7 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     // each workgroup loops over its K/V head's query heads.
     const int R = p->heads_q / p->heads_kv;
     const int64_t part = (int64_t)a.Ukv * p->seqlen_k * dp * 4;  // one group's dK (or dV) partials
-    a.G = (MFA_BWD_HEAD_SPLIT && R > 1 && 2 * R * part <= ((int64_t)2 << 30)) ? R : 1;
+    a.G = (!f32 && MFA_BWD_HEAD_SPLIT && R > 1 && 2 * R * part <= ((int64_t)2 << 30)) ? R : 1;
     if (a.G > 1 && dp > 64 && MFA_BWD_DKDV8) {
         // The eight-wavefront dK/dV kernel (one workgroup per CU) needs fewer
         // workgroups than the partials' traffic is worth: the fewest groups
@@ -1388,8 +1790,9 @@ int make_bplan(const mfa_bwd_params* bp, BPlan* plan) {
     const int64_t part_bytes = a.G > 1 ? 2 * a.G * part : 0;
     plan->ws_bytes = plan->empty ? 0 : plan->dsum_bytes + part_bytes;
     const int64_t g1 = (int64_t)f.U * ((p->seqlen_q + 15) / 16);
-    const int64_t g2 = (int64_t)a.Ukv * a.G * ((p->seqlen_k + 127) / 128);
-    const int64_t g3 = (int64_t)f.U * ((p->seqlen_q + 127) / 128);
+    const int kt = plan->k.dkdv_keys, qt = plan->k.dq_rows;
+    const int64_t g2 = (int64_t)a.Ukv * a.G * ((p->seqlen_k + kt - 1) / kt);
+    const int64_t g3 = (int64_t)f.U * ((p->seqlen_q + qt - 1) / qt);
     if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL)
         return bset_err(MFA_ERR_INVALID, "mfa_bwd: problem too large");
     plan->grid_dsum = (int)g1;
@@ -1408,7 +1811,7 @@ extern "C" {
 int mfa_bwd_params_size(void) { return (int)sizeof(mfa_bwd_params); }
 
 int mfa_bwd_supported(int32_t dtype_in, int32_t head_dim) {
-    if (dtype_in != MFA_DTYPE_F16 && dtype_in != MFA_DTYPE_BF16) return 0;
+    if (dtype_in != MFA_DTYPE_F16 && dtype_in != MFA_DTYPE_BF16 && dtype_in != MFA_DTYPE_F32) return 0;
     return head_dim > 0 && head_dim <= MFA_MAX_HEAD_DIM && head_dim % 8 == 0;
 }
 
@@ -1440,10 +1843,10 @@ int mfa_bwd(const mfa_bwd_params* params, void* workspace, int64_t workspace_byt
     const hipStream_t st = static_cast<hipStream_t>(stream);
     a.T = (params->fwd.seqlen_q + 15) / 16;
     hipLaunchKernelGGL(plan.k.dsum, dim3(plan.grid_dsum), dim3(kBThreads), 0, st, a);
-    a.T = (params->fwd.seqlen_k + 127) / 128;
+    a.T = (params->fwd.seqlen_k + plan.k.dkdv_keys - 1) / plan.k.dkdv_keys;
     hipLaunchKernelGGL(plan.k.dkdv, dim3(plan.grid_dkdv), dim3(plan.k.dkdv_threads), 0, st, a);
     if (a.G > 1) hipLaunchKernelGGL(plan.k.dkdv_sum, dim3(plan.grid_dkdv_sum), dim3(kBThreads), 0, st, a);
-    a.T = (params->fwd.seqlen_q + 127) / 128;
+    a.T = (params->fwd.seqlen_q + plan.k.dq_rows - 1) / plan.k.dq_rows;
     hipLaunchKernelGGL(plan.k.dq, dim3(plan.grid_dq), dim3(kBThreads), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return bset_err(MFA_ERR_LAUNCH, "mfa_bwd: launch failed: %s", hipGetErrorString(e));

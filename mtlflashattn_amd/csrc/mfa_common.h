@@ -304,6 +304,32 @@ __device__ __forceinline__ int64_t kv_block_off(const KArgs& a, const SeqView& s
     return (int64_t)(ok ? pg : 0) * bstride + (int64_t)(j - idx * a.page) * sstride;
 }
 
+// tanh to within 2 ulp: the odd Taylor series of tanh through t^17 below
+// |y| = 0.6 (the next term is below 3e-8 of the result there), and
+// 1 - 2 / (exp(2|y|) + 1) above it, where the difference no longer cancels
+// (the exponential form loses the small values' relative precision: near
+// y = 0 it is off by up to 1.4e-7 absolute)
+__device__ __forceinline__ float precise_tanh(float y) {
+    const float t = fabsf(y);
+    float r;
+    if (t < 0.6f) {
+        const float u = t * t;
+        float p = 6404582.f / 10854718875.f;  // coefficients of t^17, t^15, ..., t^3
+        p = fmaf(p, u, -929569.f / 638512875.f);
+        p = fmaf(p, u, 21844.f / 6081075.f);
+        p = fmaf(p, u, -1382.f / 155925.f);
+        p = fmaf(p, u, 62.f / 2835.f);
+        p = fmaf(p, u, -17.f / 315.f);
+        p = fmaf(p, u, 2.f / 15.f);
+        p = fmaf(p, u, -1.f / 3.f);
+        r = fmaf(t * u, p, t);
+    } else {
+        r = 1.f - __fdiv_rn(2.f, fast_exp2(t * (2.f * kLog2e)) + 1.f);
+    }
+    return copysignf(r, y);
+}
+
+
 // Valid key interval [lo, hi] of the query with bottom-right center `c`
 // (_kernel.py:56-64).  Window bounds are clamped on the host so c+wr cannot
 // overflow.

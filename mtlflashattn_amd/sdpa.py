@@ -105,8 +105,9 @@ def _eligibility(q, k, v, attn_mask, dropout_p, is_causal):
         return False, "batch-or-heads-mismatch"
     if k.shape[2] != v.shape[2]:
         return False, "kv-len-mismatch"
-    # the HIP backward takes bf16/fp16 only: fp32 calls that autograd will
-    # differentiate stay on stock SDPA (its gradients flow)
+    # fp32 calls that autograd will differentiate stay on stock SDPA (its
+    # gradients flow): the HIP fp32 backward is exact but runs on the vector
+    # ALU, not the matrix cores
     if q.dtype == torch.float32 and torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
         return False, "grad-fp32"
     Lq, Lk = q.shape[2], k.shape[2]

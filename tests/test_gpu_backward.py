@@ -182,12 +182,74 @@ def test_sdpa_patch_carries_gradients(monkeypatch):
     check_grads([g.transpose(1, 2) for g in got], ref, torch.bfloat16, "sdpa", factor=2.0)
 
 
-def test_fp32_backward_is_not_implemented():
-    q, k, v = make_qkv(1, 16, 16, 2, 2, 64, torch.float32, seed=13)
-    q.requires_grad_(True)
-    out = mfa.flash_attn_func(q, k, v)
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+# fp32 gradients of fp32 inputs (the fp32 kernels: fp32 end to end), against
+# float64 autograd of the oracle: within FP32_GRAD_REL * max|ref grad|.
+FP32_GRAD_REL = 5e-6  # (measured: at most 1.1e-6 over these cases)
+
+
+def check_fp32_grads(got, ref, what):
+    errs = []
+    for name, g, r in zip(("dq", "dk", "dv"), got, ref):
+        assert g.dtype == torch.float32 and g.shape == r.shape, (what, name)
+        e = rel_err(g, r)
+        errs.append(e)
+        assert e <= FP32_GRAD_REL, f"{what} {name}: rel err {e:.2e} > {FP32_GRAD_REL:.0e}"
+    return errs
+
+
+@pytest.mark.parametrize("feat", FEATURES, ids=[str(i) for i in range(len(FEATURES))])
+@pytest.mark.parametrize("shape", [(2, 200, 333, 4, 2, 64), (1, 300, 150, 2, 2, 128), (1, 130, 170, 2, 1, 40),
+                                   (1, 90, 70, 3, 3, 96)], ids=["lq<lk-gqa", "lq>lk-d128", "d40-mqa", "d96"])
+def test_fp32_grads_match_oracle(feat, shape):
+    B, Lq, Lk, Hq, Hkv, D = shape
+    q, k, v = make_qkv(B, Lq, Lk, Hq, Hkv, D, torch.float32, seed=Lq + D)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(7)).to(DEV)
+    kw = dict(feat)
+    if kw.pop("alibi", False):
+        kw["alibi_slopes"] = torch.linspace(0.05, 0.4, Hq, device=DEV)
+    _, *got = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, **kw), q, k, v, dout)
+    ref = chunked.attention_grads(q, k, v, dout, kw.get("softmax_scale"), kw.get("causal", False),
+                                  kw.get("window_size", (-1, -1)), kw.get("softcap", 0.0),
+                                  kw["alibi_slopes"].cpu() if "alibi_slopes" in kw else None, dtype=torch.float64)
+    errs = check_fp32_grads(got, ref, f"fp32 {feat} {shape}")
+    print(f"\n[bwd fp32] {feat} {shape} rel err dq/dk/dv = " + ", ".join(f"{e:.2e}" for e in errs))
+
+
+def test_fp32_lse_gradient():
+    # a loss on the returned lse enters the row sums (Dsum - dlse)
+    q, k, v = make_qkv(1, 100, 120, 2, 2, 64, torch.float32, seed=21)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(21)).to(DEV)
+    dlse = torch.randn(1, 2, 100, generator=torch.Generator().manual_seed(22)).to(DEV)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    out, lse = mfa.flash_attn_func_with_lse(qg, kg, vg, causal=True)
+    ((out * dout).sum() + (lse * dlse).sum()).backward()
+    ref = chunked.attention_grads(q, k, v, dout, causal=True, dtype=torch.float64, dlse=dlse)
+    check_fp32_grads((qg.grad, kg.grad, vg.grad), ref, "fp32 lse gradient")
+
+
+def test_fp32_varlen_grads():
+    lens_q, lens_k = [5, 0, 130, 1, 64], [9, 7, 200, 0, 64]
+    q, k, v, cu_q, cu_k = make_varlen(lens_q, lens_k, 4, 2, 64, torch.float32, seed=23)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(23)).to(DEV)
+    f = lambda q, k, v: mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens_q), max(lens_k),  # noqa: E731
+                                                   causal=True, softcap=6.0)
+    _, *got = grads_of(f, q, k, v, dout)
+    ref = chunked.attention_grads_varlen(q, k, v, dout, cu_q.cpu(), cu_k.cpu(), causal=True, softcap=6.0,
+                                         dtype=torch.float64)
+    check_fp32_grads(got, ref, "fp32 varlen")
+    _, *again = grads_of(f, q, k, v, dout)
+    assert all(torch.equal(a, b) for a, b in zip(got, again))  # no atomics: bit-identical
+    sq = [0] + torch.tensor(lens_q).cumsum(0).tolist()
+    sk = [0] + torch.tensor(lens_k).cumsum(0).tolist()
+    for i in range(len(lens_q)):
+        if lens_q[i] == 0 or lens_k[i] == 0:
+            continue
+        a, b, c, d = sq[i], sq[i + 1], sk[i], sk[i + 1]
+        _, dq, dk, dv = grads_of(lambda q, k, v: mfa.flash_attn_func(q, k, v, causal=True, softcap=6.0),
+                                 q[None, a:b], k[None, c:d], v[None, c:d], dout[None, a:b])
+        assert torch.equal(got[0][a:b], dq[0]) and torch.equal(got[1][c:d], dk[0]) and \
+            torch.equal(got[2][c:d], dv[0]), f"sequence {i}"
+    assert (got[1][sk[1]:sk[2]] == 0).all() and (got[2][sk[1]:sk[2]] == 0).all()
 
 
 def test_gqa_grads_equal_summed_repeated_heads():

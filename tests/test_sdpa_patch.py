@@ -78,8 +78,8 @@ class TestGates:
             sdpa.uninstall()
 
     def test_fp32_under_autograd_stays_stock(self):
-        # the HIP backward takes bf16/fp16 only: fp32 calls whose inputs need
-        # gradients go to stock SDPA, 16-bit ones keep the kernel
+        # fp32 calls whose inputs need gradients go to stock SDPA (the HIP
+        # fp32 backward runs on the vector ALU), 16-bit ones keep the kernel
         assert sdpa.install()
         try:
             q = torch.zeros(1, 2, 1024, 64, dtype=torch.float32, requires_grad=True)
