@@ -60,6 +60,11 @@ def test_supported_table(lib):
         assert all(lib.mfa_supported(dt, d) for d in (8, 32, 64, 96, 128))
         assert not lib.mfa_supported(dt, 130) and not lib.mfa_supported(dt, 33) and not lib.mfa_supported(dt, 0)
     assert not lib.mfa_supported(7, 64)
+    # the backward: the same table (fp32 on its vector-ALU kernels)
+    for dt in (_hip.MFA_DTYPE_F16, _hip.MFA_DTYPE_BF16, _hip.MFA_DTYPE_F32):
+        assert all(lib.mfa_bwd_supported(dt, d) for d in (8, 32, 64, 96, 128))
+        assert not lib.mfa_bwd_supported(dt, 130) and not lib.mfa_bwd_supported(dt, 33)
+    assert not lib.mfa_bwd_supported(7, 64)
 
 
 def good_params(B=1, L=256, H=4, Hkv=4, D=64, dtype=_hip.MFA_DTYPE_BF16):
