@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MFA_ABI_VERSION 6
+#define MFA_ABI_VERSION 7
 
 /* element types (dtype_in / dtype_out) */
 #define MFA_DTYPE_F16 0
@@ -162,6 +162,14 @@ typedef struct mfa_fwd_params {
     int64_t block_table_batch_stride;
     int32_t page_block_size;
     int32_t num_pages;
+
+    /* Varlen calls, optional (0 = unknown; ABI 7): 1 when the caller knows
+     * that no sequence has exactly one query row.  A varlen call otherwise
+     * adds a launch of the exact-row kernel for such sequences (the main
+     * launch leaves them to it); 1 skips that launch, so a sequence of one
+     * query row would keep its o rows (and lse) unwritten.  Ignored by dense
+     * calls.  No counterpart in the reference. */
+    int32_t varlen_no_single_rows;
 } mfa_fwd_params;
 
 /* Launch geometry of one mfa_fwd call (for profiling/roofline reports). */

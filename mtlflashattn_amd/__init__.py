@@ -226,10 +226,12 @@ def _varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale, causal, window_s
         _check_block_table(block_table, lens_k, k.shape[1], k.shape[0])
 
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    # (with no sequence of exactly one query row, the launch for such rows is skipped)
     return forward_varlen(
         q, k, v, cu_seqlens_q, cu_seqlens_k, max(lens_q, default=0), max(lens_k, default=0),
         scale=scale, causal=causal, softcap=softcap, window_left=window_size[0],
         window_right=window_size[1], alibi_slopes=alibi_slopes, return_lse=return_lse, block_table=block_table,
+        no_single_rows=1 not in lens_q,
     )
 
 

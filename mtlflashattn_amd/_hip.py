@@ -21,7 +21,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime first)
 
 from ._build import LIB_PATH
 
-MFA_ABI_VERSION = 6
+MFA_ABI_VERSION = 7
 MFA_DTYPE_F16 = 0
 MFA_DTYPE_BF16 = 1
 MFA_DTYPE_F32 = 2
@@ -63,7 +63,7 @@ class MfaFwdParams(ctypes.Structure):
         ("dtype_in", _c_i32), ("dtype_out", _c_i32), ("tile_hint", _c_i32),
         ("softmax_lse", _c_ptr), ("lse_batch_stride", _c_i64), ("lse_head_stride", _c_i64),
         ("block_table", _c_ptr), ("block_table_batch_stride", _c_i64),
-        ("page_block_size", _c_i32), ("num_pages", _c_i32),
+        ("page_block_size", _c_i32), ("num_pages", _c_i32), ("varlen_no_single_rows", _c_i32),
     ]
 
 

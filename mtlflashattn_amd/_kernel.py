@@ -206,7 +206,7 @@ def _strides_bsh(x: torch.Tensor):
 
 
 def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, alibi, alibi_bstride,
-         cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None, lse=None, block_table=None):
+         cu_q=None, cu_k=None, seqlen_q=None, seqlen_k=None, lse=None, block_table=None, no_single_rows=False):
     """Launch the HIP forward on [B, S, H, D] views q, k, v and write `out`.
 
     out: [B, Sq, Hq, D] tensor of q.dtype or float32 (full-precision output).
@@ -217,6 +217,8 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     block_table: optional int32 [batch, pages per sequence] page table; k/v
     are then [num_pages, page_block_size, Hkv, D] and every sequence's key
     count comes from seqlen_k (dense) or cu_k (varlen).
+    no_single_rows: (varlen) no sequence has exactly one query row, so the
+    exact-row launch for such sequences is skipped.
     """
     _kernel_mode()
     B, Sq, Hq, D = q.shape
@@ -260,6 +262,7 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
                 p.softmax_lse = lse.data_ptr()
             if paged is not None:
                 p.block_table = block_table.data_ptr()
+            p.varlen_no_single_rows = 1 if (varlen and no_single_rows) else 0
             _launch(p, ent[1], q.device)
             return out
     if Dp != D:  # the kernels read 16-byte chunks: zero-pad the head dim
@@ -298,6 +301,7 @@ def _run(q, k, v, out, *, scale, causal, softcap, window_left, window_right, ali
     if paged is not None:
         p.block_table = block_table.data_ptr()
         p.block_table_batch_stride, p.page_block_size, p.num_pages = paged
+    p.varlen_no_single_rows = 1 if (varlen and no_single_rows) else 0
     _launch(p, _split_choice(p, q.dtype, hint), q.device)
     if dst is not out:
         out.copy_(dst[..., :D])
@@ -447,7 +451,7 @@ def forward_bshd(q, k, v, scale, causal, softcap=0.0, window_left=-1, window_rig
 
 def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0, window_left=-1,
                    window_right=-1, alibi_slopes=None, out_dtype=None, return_lse=False, block_table=None,
-                   _grad=True):
+                   _grad=True, no_single_rows=False):
     """Packed varlen forward in ONE launch: q [Tq,Hq,D], k/v [Tk,Hkv,D].
 
     cu_q/cu_k: int32 [batch+1] device tensors; max_q/max_k: the longest
@@ -457,7 +461,10 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
     [batch, pages per sequence]; k/v are then a page pool
     [num_pages, page_block_size, Hkv, D] and cu_k gives the key counts only
     (paged calls are forward-only).  Inputs that require grad (and no block
-    table, q.dtype output) go through the HIP backward.
+    table, q.dtype output) go through the HIP backward.  no_single_rows: the
+    caller knows no sequence has exactly one query row (the library then
+    skips the exact-row launch for such sequences; a one-row sequence would
+    be left unwritten).
     """
     batch = cu_q.shape[0] - 1
     Hq = q.shape[1]
@@ -474,7 +481,7 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
                                   "run them under torch.no_grad() or without inputs that require grad")
     if _grad and block_table is None and _needs_grad(q, k, v) and _out_dtype(q, out_dtype) == q.dtype:
         o, lse = _FlashAttnVarlenFn.apply(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left,
-                                          window_right, alibi_slopes)
+                                          window_right, alibi_slopes, no_single_rows)
         return (o, lse) if return_lse else o
     out = torch.empty(q.shape, dtype=_out_dtype(q, out_dtype), device=q.device)
     lse = torch.empty(Hq, q.shape[0], dtype=torch.float32, device=q.device) if return_lse else None
@@ -487,7 +494,7 @@ def forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap=0.0
     _run(q[None], k if block_table is not None else k[None], v if block_table is not None else v[None], out[None],
          scale=scale, causal=causal, softcap=softcap, window_left=window_left, window_right=window_right,
          alibi=alibi, alibi_bstride=bstride, cu_q=cu_q, cu_k=cu_k, seqlen_q=max_q, seqlen_k=max_k, lse=lse,
-         block_table=block_table)
+         block_table=block_table, no_single_rows=no_single_rows)
     return (out, lse) if return_lse else out
 
 
@@ -605,9 +612,10 @@ class _FlashAttnVarlenFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left, window_right,
-                alibi_slopes):
+                alibi_slopes, no_single_rows=False):
         out, lse = forward_varlen(q, k, v, cu_q, cu_k, max_q, max_k, scale, causal, softcap, window_left,
-                                  window_right, alibi_slopes, return_lse=True, _grad=False)
+                                  window_right, alibi_slopes, return_lse=True, _grad=False,
+                                  no_single_rows=no_single_rows)
         batch, Hq = cu_q.shape[0] - 1, q.shape[1]
         alibi, bstride = _alibi_arg(alibi_slopes, batch, Hq, q.device)
         cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
@@ -626,7 +634,7 @@ class _FlashAttnVarlenFn(torch.autograd.Function):
             dout = torch.zeros_like(out)
         dq, dk, dv = _run_bwd(q[None], k[None], v[None], out[None], dout[None], lse, cu_q=cu_q, cu_k=cu_k,
                               dlse=dlse, **ctx.cfg)
-        return dq[0], dk[0], dv[0], None, None, None, None, None, None, None, None, None, None
+        return dq[0], dk[0], dv[0], None, None, None, None, None, None, None, None, None, None, None
 
 
 def split_chunk(q, k):

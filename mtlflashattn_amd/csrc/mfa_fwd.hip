@@ -2604,7 +2604,8 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     // (a second launch, planned below), so each sequence's rows are those of
     // its own dense call.
     const bool exact_call = din != MFA_DTYPE_F32 && (pack || p->seqlen_q == 1);
-    const bool mixed_rows = din != MFA_DTYPE_F32 && !exact_call && p->cu_seqlens_q != nullptr;
+    const bool mixed_rows =
+        din != MFA_DTYPE_F32 && !exact_call && p->cu_seqlens_q != nullptr && !p->varlen_no_single_rows;
     // At most 32 keys per sequence under many query rows (cross-attention to
     // a short conditioning sequence): the tiny-key kernel, which keeps the
     // keys in registers and streams the query rows (measured at bf16 D=128

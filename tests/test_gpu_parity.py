@@ -280,6 +280,18 @@ class TestVarlen:
         out2 = mfa.flash_attn_varlen_func(q2, k2, v2, cu_q, cu_k, max(lens), max(lens), causal=True)
         assert torch.equal(out2[starts[1]:starts[2]], out[starts[1]:starts[2]])
 
+    @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+    def test_no_single_rows_flag(self, dtype):
+        # with no sequence of one query row, the API skips the exact-row
+        # launch (varlen_no_single_rows): the same bits as with it
+        lens = [96, 257, 2, 130]
+        q, k, v, cu_q, cu_k = make_varlen(lens, lens, 8, 2, 64, dtype, seed=5)
+        a = _kernel.forward_varlen(q, k, v, cu_q, cu_k, 257, 257, 0.125, True, return_lse=True, no_single_rows=True)
+        b = _kernel.forward_varlen(q, k, v, cu_q, cu_k, 257, 257, 0.125, True, return_lse=True)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        assert torch.equal(mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, 257, 257, causal=True, softmax_scale=0.125),
+                           b[0])
+
     def test_mismatched_batch_raises(self):
         q, k, v, cu_q, _ = make_varlen([32, 32], [32, 32], 4, 4, 64, torch.float16)
         cu_k_bad = torch.tensor([0, 64], dtype=torch.int32, device="cuda")
