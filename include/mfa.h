@@ -278,7 +278,7 @@ typedef struct mfa_bwd_params {
     /* q, k, v, o (the forward output), shapes, strides, masks and biases as
      * in the forward; fwd.softmax_lse (+ strides) is the forward's lse and
      * required; fwd.block_table must be NULL; fwd.tile_hint is ignored;
-     * fwd.dtype_out is o's dtype (dtype_in or fp32). */
+     * fwd.dtype_out is o's dtype and must equal dtype_in. */
     mfa_fwd_params fwd;
     const void* dout; /* dL/dO, laid out like o (its own strides), o's dtype */
     int64_t do_batch_stride, do_seq_stride, do_head_stride;
