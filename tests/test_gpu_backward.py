@@ -199,7 +199,8 @@ def check_fp32_grads(got, ref, what):
 
 @pytest.mark.parametrize("feat", FEATURES, ids=[str(i) for i in range(len(FEATURES))])
 @pytest.mark.parametrize("shape", [(2, 200, 333, 4, 2, 64), (1, 300, 150, 2, 2, 128), (1, 130, 170, 2, 1, 40),
-                                   (1, 90, 70, 3, 3, 96)], ids=["lq<lk-gqa", "lq>lk-d128", "d40-mqa", "d96"])
+                                   (1, 90, 70, 3, 3, 96), (1, 50, 60, 2, 2, 33)],
+                         ids=["lq<lk-gqa", "lq>lk-d128", "d40-mqa", "d96", "d33"])
 def test_fp32_grads_match_oracle(feat, shape):
     B, Lq, Lk, Hq, Hkv, D = shape
     q, k, v = make_qkv(B, Lq, Lk, Hq, Hkv, D, torch.float32, seed=Lq + D)
