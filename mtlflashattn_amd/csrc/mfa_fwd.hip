@@ -479,15 +479,16 @@ __device__ __forceinline__ void store_out_l(const KArgs& a, const SeqView& sv, f
                 const float v2 = o[qb][db][4 * g + 2] * inv, v3 = o[qb][db][4 * g + 3] * inv;
                 if (a.out_f32) {
                     float* dst = reinterpret_cast<float*>(sv.o) + (int64_t)qrow * a.os + d;
-                    *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+                    typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4v_t;
+                    store_stream(reinterpret_cast<f32x4v_t*>(dst), f32x4v_t{v0, v1, v2, v3});
                 } else if constexpr (IS_BF16) {
                     typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
                     bf16x4_t w = {(__bf16)v0, (__bf16)v1, (__bf16)v2, (__bf16)v3};
-                    *reinterpret_cast<bf16x4_t*>(reinterpret_cast<__bf16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+                    store_stream(reinterpret_cast<bf16x4_t*>(reinterpret_cast<__bf16*>(sv.o) + (int64_t)qrow * a.os + d), w);
                 } else {
                     typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4_t;
                     f16x4_t w = {(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
-                    *reinterpret_cast<f16x4_t*>(reinterpret_cast<_Float16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+                    store_stream(reinterpret_cast<f16x4_t*>(reinterpret_cast<_Float16*>(sv.o) + (int64_t)qrow * a.os + d), w);
                 }
             }
     }
@@ -556,7 +557,7 @@ __device__ __forceinline__ void store_out_rows(const KArgs& a, const SeqView& sv
         const int ch = lane + 64 * i, r = ch / CPR, col = (ch % CPR) * 8;
         const u32x4_t w = *reinterpret_cast<const u32x4_t*>(ls + r * ST + col);
         const int qrow = qrow0 + r;
-        if (qrow < sv.Lq && col < a.D) *reinterpret_cast<u32x4_t*>(sv.o + ((int64_t)qrow * a.os + col) * 2) = w;
+        if (qrow < sv.Lq && col < a.D) store_stream(reinterpret_cast<u32x4_t*>(sv.o + ((int64_t)qrow * a.os + col) * 2), w);
     }
 }
 
@@ -644,13 +645,15 @@ __global__ void __launch_bounds__(64) mfa_combine_kernel(KArgs a) {
         acc1 /= wsum;
     }
     if (a.out_f32) {
-        *reinterpret_cast<float2*>(reinterpret_cast<float*>(sv.o) + (int64_t)qrow * a.os + d) = make_float2(acc0, acc1);
+        typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2v_t;
+        store_stream(reinterpret_cast<f32x2v_t*>(reinterpret_cast<float*>(sv.o) + (int64_t)qrow * a.os + d),
+                     f32x2v_t{acc0, acc1});
     } else if constexpr (IS_BF16) {
         const bf16x2_t w = {(__bf16)acc0, (__bf16)acc1};
-        *reinterpret_cast<bf16x2_t*>(reinterpret_cast<__bf16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+        store_stream(reinterpret_cast<bf16x2_t*>(reinterpret_cast<__bf16*>(sv.o) + (int64_t)qrow * a.os + d), w);
     } else {
         const f16x2_t w = {(_Float16)acc0, (_Float16)acc1};
-        *reinterpret_cast<f16x2_t*>(reinterpret_cast<_Float16*>(sv.o) + (int64_t)qrow * a.os + d) = w;
+        store_stream(reinterpret_cast<f16x2_t*>(reinterpret_cast<_Float16*>(sv.o) + (int64_t)qrow * a.os + d), w);
     }
 }
 
@@ -1918,7 +1921,7 @@ mfa_fwd16_tk_kernel(KArgs a) {
             const int ch = lane + 64 * i, orow = wq0 + ch / CPR, col = (ch % CPR) * 8;
             const u32x4_t w = *reinterpret_cast<const u32x4_t*>(qo + (ch / CPR) * KST + col);
             if (orow < Lq && col < D)
-                *reinterpret_cast<u32x4_t*>(sv.o + ((int64_t)orow * a.os + col) * 2) = w;
+                store_stream(reinterpret_cast<u32x4_t*>(sv.o + ((int64_t)orow * a.os + col) * 2), w);
         }
     }
 }
