@@ -1418,7 +1418,9 @@ mfa_fwd16_pp_kernel(KArgs a) {
         const int64_t bo = kv_block_off<false>(a, sv, j, Lk, bstride, stride, ok);
         int bytes = full;
         if (rows < BN) bytes = rows > 0 ? ((rows - 1) * (int)stride + D) * 2 : 0;
-        if (!ok || j0 < jbeg) bytes = 0;
+        // steps past the walk load nothing (under causal masks their blocks
+        // can lie inside the sequence, and their reads would be wasted)
+        if (!ok || j0 < jbeg || u >= nblk) bytes = 0;
         lds_load16(reinterpret_cast<uint64_t>(base + bo * 2), (uint32_t)bytes, dst, off);
     };
     // loads of K block u into its stage u % NST (and likewise V); wave-uniform
