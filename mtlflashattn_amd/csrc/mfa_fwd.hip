@@ -39,6 +39,8 @@
 //    than a factor 2 (a wave-uniform branch); the reference max then becomes
 //    every row's exact max, so probabilities stay <= 2 and the row's largest
 //    weight is within one binade of 1.0 when P is rounded to 16 bits.
+//  * O leaves through non-temporal stores (row-contiguous 16-byte pieces,
+//    staged through LDS, in the 16-bit kernels): it is never read back here.
 //  * Where the number of K/V head groups is a multiple of 8, all tiles of one
 //    K/V head run on one XCD, so its K/V stays in that XCD's L2: one
 //    (sequence, q head) after another when tiles cost the same, heaviest
