@@ -2510,9 +2510,11 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     bool fills_chip = pp_hint;
     if (p->tile_hint == MFA_TILE_AUTO) {
         if (dp == 128) {
-            // Rows long enough: >= 8 tiles per head, 16 when causal (measured:
-            // B=32 Lq=256 44 vs 40 us, B=16 Lq=1024 causal 145 vs 116 on the
-            // ping-pong tiles).  All 8 wavefronts of a ping-pong workgroup walk
+            // Rows long enough: >= 2 tiles per head, 8 when causal (bf16,
+            // ping-pong vs 4-wavefront, one box: non-causal B=64 L=256 64 vs
+            // 61 us, B=32 L=512 88 vs 93, B=4 L=768 28 vs 32, B=16 L=1024 143
+            // vs 157; causal B=16 L=1024 113 vs 111, B=16 L=1536 221 vs 219,
+            // B=8 L=2048 166 vs 176, B=4 L=3072 177 vs 180).  All 8 wavefronts of a ping-pong workgroup walk
             // the key range of all its 256 rows, so a sliding window must be
             // wide against that: windows of >= 2048 keys run 3-13% faster there
             // (L=8192 (1024,1024) 145 vs 154 us, (4096,0) causal 234 vs 241,
@@ -2520,10 +2522,12 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             // ((256,256) 67 vs 61, (512,0) causal 67 vs 61).  A soft-cap /
             // ALiBi transform under a window stays on the 4-wavefront kernel
             // (L=32768 H=16 causal (2048,0) with soft-cap 30 and ALiBi: 832 vs
-            // 791 us).  Varlen calls give only the longest sequence: the
-            // non-causal threshold rises to 12 tiles (8 lengths in [863, 3501]
-            // at Hq=32 Hkv=8: non-causal 798 vs 870 us; 32 lengths in
-            // [128, 2048]: 828 vs 751).
+            // 791 us).  Varlen calls give only the longest sequence, and short
+            // sequences waste half-empty 256-row tiles: the thresholds rise to
+            // 5 tiles non-causal and 16 causal (H=16: 64 lengths in [128,
+            // 1024] 338 vs 304 us, 32 in [256, 1280] 273 vs 283, 32 in [128,
+            // 2048] 380 vs 373, 16 in [512, 1536] 175 vs 184; causal 16 in
+            // [512, 1536] 129 vs 118, 8 in [1024, 4096] 298 vs 301).
             // A grouped-query call with 2, 4 or 8 query heads per K/V head
             // packs them into each tile (256 / R positions per ping-pong
             // tile): there rows of >= 2048 positions go to the ping-pong
@@ -2545,7 +2549,9 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             const int64_t left = p->window_left >= 0 ? p->window_left : inf;
             const int64_t right = p->causal ? 0 : p->window_right >= 0 ? p->window_right : inf;
             const bool windowed = p->window_left >= 0 || p->window_right >= 0;
-            const int64_t min_tiles = packs ? (2048 + pos_pp - 1) / pos_pp : p->causal ? 16 : p->cu_seqlens_q ? 12 : 8;
+            const int64_t min_tiles = packs              ? (2048 + pos_pp - 1) / pos_pp
+                                      : p->cu_seqlens_q ? (p->causal ? 16 : 5)
+                                                        : (p->causal ? 8 : 2);
             fills_chip = units_pp * t256 >= geom.cus && 4 * rows_pp <= 5 * rows_4w && t256 >= min_tiles &&
                          (!windowed || (!bias && left + right + 1 >= 2048));
         } else

@@ -211,8 +211,17 @@ def test_launch_geometry_of_the_baseline_configs(lib):
         b"mfa_fwd16<f16,d128")
     assert _kernel.launch_info(f16, f16, f16, causal=True, softcap=30.0, window_left=4096,
                                window_right=0).kernel_name.startswith(b"mfa_fwd16<f16,d128")
-    short128 = torch.empty(16, 1024, 16, 128, dtype=torch.float16)  # 4 tiles per head
-    assert _kernel.launch_info(short128, short128, short128, causal=True).kernel_name.startswith(b"mfa_fwd16<f16,d128")
+    # dense rows: >= 2 tiles of 256 rows per head go to the ping-pong tiles,
+    # >= 8 when causal
+    def d128(B, L, causal):
+        t = torch.empty(B, L, 16, 128, dtype=torch.float16)
+        return _kernel.launch_info(t, t, t, causal=causal).kernel_name
+    assert d128(64, 256, False).startswith(b"mfa_fwd16<f16,d128")  # 1 tile per head
+    assert d128(32, 512, False).startswith(b"mfa_fwd16pp<f16,d128")
+    assert d128(16, 1024, True).startswith(b"mfa_fwd16<f16,d128")  # 4 tiles per head
+    assert d128(16, 1536, True).startswith(b"mfa_fwd16<f16,d128")  # 6
+    assert d128(8, 2048, True).startswith(b"mfa_fwd16pp<f16,d128")  # 8
+    assert d128(32, 384, False).startswith(b"mfa_fwd16<f16,d128")  # 512 padded rows against 384
     small128 = torch.empty(1, 2048, 16, 128, dtype=torch.float16)
     assert _kernel.launch_info(small128, small128, small128).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     big = torch.empty(1, 32768, 16, 128, dtype=torch.bfloat16)
@@ -226,7 +235,7 @@ def test_launch_geometry_of_the_baseline_configs(lib):
 
 def test_varlen_d128_kernel_choice(lib):
     # varlen calls give the longest sequence only: at head dim 128 the
-    # ping-pong tiles need >= 12 tiles of 256 rows non-causal, 16 causal;
+    # ping-pong tiles need >= 5 tiles of 256 rows non-causal, 16 causal;
     # grouped-query calls whose tiles pack 2, 4 or 8 query heads need rows
     # of >= 2048 positions
     def varlen(nseq, longest, Hq, Hkv, causal):
@@ -242,6 +251,9 @@ def test_varlen_d128_kernel_choice(lib):
     assert varlen(64, 1024, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")
     assert varlen(8, 3501, 16, 16, True).startswith(b"mfa_fwd16<bf16,d128")  # one head per K/V head: 14 < 16
     assert varlen(4, 8192, 16, 16, True).startswith(b"mfa_fwd16pp<bf16,d128")
+    assert varlen(64, 1024, 16, 16, False).startswith(b"mfa_fwd16<bf16,d128")  # 4 tiles
+    assert varlen(32, 1280, 16, 16, False).startswith(b"mfa_fwd16pp<bf16,d128")  # 5 tiles
+    assert varlen(16, 2048, 16, 16, True).startswith(b"mfa_fwd16<bf16,d128")  # causal: 8 < 16
     # the Python helper plans the same call (config 4's geometry)
     q = torch.empty(18373, 32, 128, dtype=torch.bfloat16)
     k = torch.empty(18373, 8, 128, dtype=torch.bfloat16)

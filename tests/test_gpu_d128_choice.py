@@ -1,9 +1,10 @@
 """Head dim 128 calls that the automatic choice sends to the ping-pong tiles
 because their key ranges are long: sliding windows of >= 2048 keys without a
-soft-cap / ALiBi transform, and varlen calls whose longest sequence has >= 12
-tiles (16 when causal) -- of 256 rows, or of 256 / R positions when the
-tiles pack R = 2, 4 or 8 query heads of one K/V head.  Each case checks the kernel the library
-picks (launch_info / the plan's name) and the result against the oracle
+soft-cap / ALiBi transform, varlen calls whose longest sequence has >= 5
+tiles (16 when causal) and dense rows of >= 2 tiles (8 when causal) -- of 256
+rows, or of 256 / R positions when the tiles pack R = 2, 4 or 8 query heads
+of one K/V head.  Each case checks the kernel the library picks
+(launch_info / the plan's name) and the result against the oracle
 (_kernel.py:1188-1207's mask order), in the fp32 parity
 output and the 16-bit output; the 4-wavefront kernel on the same call meets
 the same bars."""
@@ -47,6 +48,20 @@ def test_wide_windows_take_the_pingpong_tiles(dtype, causal, ws, L, H, monkeypat
     assert_output(mfa.flash_attn_func(q, k, v, **kw)[:, sel], ref, dtype, f"pp {ws}")
     monkeypatch.setattr(_kernel, "_TILE_HINT", _hip.MFA_TILE_256)  # the kernel these calls used before
     assert_output(mfa.flash_attn_func(q, k, v, **kw)[:, sel], ref, dtype, f"4-wave {ws}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES16)
+@pytest.mark.parametrize("causal,B,L,H", [(False, 32, 512, 8), (True, 8, 2048, 4)], ids=["2-tiles", "causal-8-tiles"])
+def test_short_dense_rows_take_the_pingpong_tiles(dtype, causal, B, L, H, monkeypatch):
+    q, k, v = make_qkv(B, L, L, H, H, 128, dtype, seed=B + L)
+    info = _kernel.launch_info(q, k, v, causal=causal)
+    assert info.kernel_name.startswith(b"mfa_fwd16pp<"), info.kernel_name
+    sel = [0, B - 1]  # the oracle on the first and the last sequence
+    ref = chunked.flash_attn_func(q[sel].cpu(), k[sel].cpu(), v[sel].cpu(), chunk=512, causal=causal)
+    assert_parity(_fp32_dense(q, k, v, causal, (-1, -1))[sel], ref, dtype, "pp fp32 out")
+    assert_output(mfa.flash_attn_func(q, k, v, causal=causal)[sel], ref, dtype, "pp")
+    monkeypatch.setattr(_kernel, "_TILE_HINT", _hip.MFA_TILE_256)
+    assert_output(mfa.flash_attn_func(q, k, v, causal=causal)[sel], ref, dtype, "4-wave")
 
 
 @pytest.mark.parametrize("dtype", DTYPES16)
