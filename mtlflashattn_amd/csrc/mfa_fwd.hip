@@ -2600,15 +2600,17 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
         // B=8 L=1024 Hq=32 68 vs 97 us, B=2 L=4096 Hq=32 Hkv=8 172 vs 190;
         // with one round, or longer rows, the ping-pong tiles win: L=4096
         // H=32 100 vs 117, B=2 L=8192 H=16 327 vs 345).
-        // Non-causal rows of one 512-row tile per head go there too (bf16
+        // Rows of one 512-row tile per head go there too: non-causal (bf16
         // H=16 L=512, 4-wavefront vs ping-pong: B=32 D=64 50.2 vs 52.4 us,
         // B=64 D=64 96.7 vs 101.7, B=32 D=32 38.5 vs 42.1; at L=1024 the
-        // ping-pong tiles win, B=16 D=64 83.5 vs 87.1).
+        // ping-pong tiles win, B=16 D=64 83.5 vs 87.1), and causal ones in
+        // a single round of 512-row tiles, whose 256-row tiles would take
+        // two (B=32 L=512 H=8 D=64 23.5 vs 31.1 us).
         const bool windowed = p->window_left >= 0 || p->window_right >= 0;
         const int64_t t512 = rows512 / 512;
         if (windowed || (p->causal && bias) || p->cu_seqlens_q)
             fills_chip = false;
-        else if (p->causal && t512 <= 8 && units * t512 > geom.cus)
+        else if (p->causal && t512 <= 8 && (units * t512 > geom.cus || t512 == 1))
             fills_chip = false;
         else if (!p->causal && t512 < 2)
             fills_chip = false;

@@ -196,6 +196,8 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     for D in (32, 64):  # one 512-row tile per head: the 4-wavefront kernel
         c512 = torch.empty(32, 512, 16, D, dtype=torch.bfloat16)
         assert _kernel.launch_info(c512, c512, c512).block_x == 256
+        one_round = torch.empty(32, 512, 8, D, dtype=torch.bfloat16)  # 256 tiles of 512 rows, causal
+        assert _kernel.launch_info(one_round, one_round, one_round, causal=True).block_x == 256
     c16k = torch.empty(1, 16384, 16, 64, dtype=torch.bfloat16)  # 512 tiles: balanced by the schedule
     assert _kernel.launch_info(c16k, c16k, c16k, causal=True).rows_per_block == 512
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
