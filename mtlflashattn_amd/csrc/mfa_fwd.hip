@@ -2530,8 +2530,15 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             // [512, 1536] 129 vs 118, 8 in [1024, 4096] 298 vs 301).
             // A grouped-query call with 2, 4 or 8 query heads per K/V head
             // packs them into each tile (256 / R positions per ping-pong
-            // tile): there rows of >= 2048 positions go to the ping-pong
-            // tiles, causal or not, varlen or dense (measured at Hq=32 Hkv=8
+            // tile): there rows go to the ping-pong tiles from 512 positions
+            // when dense and non-causal, 1024 when varlen and non-causal and
+            // 1280 when causal (bf16 Hq=32 Hkv=8, 4-wavefront vs ping-pong,
+            // one box: non-causal B=32 L=512 181 vs 172 us, B=16 L=1024 317
+            // vs 286; causal B=32 L=512 135 vs 143, B=16 L=1024 200 vs 199,
+            // B=12 L=1536 295 vs 275; varlen 64 lengths in [64, 1024] 480 vs
+            // 474 and causal 313 vs 320, 32 in [128, 1536] 700 vs 649 and
+            // 420 vs 411).  All were 2048 before the ping-pong tiles got
+            // cheaper (measured at Hq=32 Hkv=8
             // D=128 on packed tiles, ping-pong vs 4-wavefront: config 4's 8
             // varlen lengths in [863, 3501] causal 474 vs 516 us, non-causal
             // 802 vs 868; 16 lengths in [256, 4096] 919 vs 997 and 1610 vs
@@ -2549,7 +2556,8 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             const int64_t left = p->window_left >= 0 ? p->window_left : inf;
             const int64_t right = p->causal ? 0 : p->window_right >= 0 ? p->window_right : inf;
             const bool windowed = p->window_left >= 0 || p->window_right >= 0;
-            const int64_t min_tiles = packs              ? (2048 + pos_pp - 1) / pos_pp
+            const int64_t min_pos = p->causal ? 1280 : p->cu_seqlens_q ? 1024 : 512;
+            const int64_t min_tiles = packs              ? (min_pos + pos_pp - 1) / pos_pp
                                       : p->cu_seqlens_q ? (p->causal ? 16 : 5)
                                                         : (p->causal ? 8 : 2);
             fills_chip = units_pp * t256 >= geom.cus && 4 * rows_pp <= 5 * rows_4w && t256 >= min_tiles &&

@@ -227,6 +227,16 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     assert d128(16, 1536, True).startswith(b"mfa_fwd16<f16,d128")  # 6
     assert d128(8, 2048, True).startswith(b"mfa_fwd16pp<f16,d128")  # 8
     assert d128(32, 384, False).startswith(b"mfa_fwd16<f16,d128")  # 512 padded rows against 384
+    # packed grouped-query tiles (4 query heads per K/V head): rows of >= 512
+    # positions, 1280 when causal
+    def gqa(B, L, causal):
+        q = torch.empty(B, L, 32, 128, dtype=torch.float16)
+        kv = torch.empty(B, L, 8, 128, dtype=torch.float16)
+        return _kernel.launch_info(q, kv, kv, causal=causal).kernel_name
+    assert gqa(32, 512, False).startswith(b"mfa_fwd16pp<f16,d128")
+    assert gqa(64, 256, False).startswith(b"mfa_fwd16<f16,d128")
+    assert gqa(16, 1024, True).startswith(b"mfa_fwd16<f16,d128")
+    assert gqa(12, 1536, True).startswith(b"mfa_fwd16pp<f16,d128")
     small128 = torch.empty(1, 2048, 16, 128, dtype=torch.float16)
     assert _kernel.launch_info(small128, small128, small128).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     big = torch.empty(1, 32768, 16, 128, dtype=torch.bfloat16)
@@ -242,7 +252,7 @@ def test_varlen_d128_kernel_choice(lib):
     # varlen calls give the longest sequence only: at head dim 128 the
     # ping-pong tiles need >= 5 tiles of 256 rows non-causal, 16 causal;
     # grouped-query calls whose tiles pack 2, 4 or 8 query heads need rows
-    # of >= 2048 positions
+    # of >= 1024 positions (1280 causal)
     def varlen(nseq, longest, Hq, Hkv, causal):
         p = good_params(B=nseq, L=longest, H=Hq, Hkv=Hkv, D=128)
         p.q_batch_stride = p.k_batch_stride = p.v_batch_stride = p.o_batch_stride = 0
@@ -253,7 +263,9 @@ def test_varlen_d128_kernel_choice(lib):
     assert varlen(8, 3501, 32, 8, True).startswith(b"mfa_fwd16pp<bf16,d128")
     assert varlen(32, 2048, 32, 8, False).startswith(b"mfa_fwd16pp<bf16,d128")
     assert varlen(64, 1024, 32, 8, True).startswith(b"mfa_fwd16<bf16,d128")
-    assert varlen(64, 1024, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")
+    assert varlen(64, 1024, 32, 8, False).startswith(b"mfa_fwd16pp<bf16,d128")
+    assert varlen(64, 960, 32, 8, False).startswith(b"mfa_fwd16<bf16,d128")  # 15 tiles of 64
+    assert varlen(64, 1280, 32, 8, True).startswith(b"mfa_fwd16pp<bf16,d128")
     assert varlen(8, 3501, 16, 16, True).startswith(b"mfa_fwd16<bf16,d128")  # one head per K/V head: 14 < 16
     assert varlen(4, 8192, 16, 16, True).startswith(b"mfa_fwd16pp<bf16,d128")
     assert varlen(64, 1024, 16, 16, False).startswith(b"mfa_fwd16<bf16,d128")  # 4 tiles

@@ -51,9 +51,11 @@ def test_wide_windows_take_the_pingpong_tiles(dtype, causal, ws, L, H, monkeypat
 
 
 @pytest.mark.parametrize("dtype", DTYPES16)
-@pytest.mark.parametrize("causal,B,L,H", [(False, 32, 512, 8), (True, 8, 2048, 4)], ids=["2-tiles", "causal-8-tiles"])
-def test_short_dense_rows_take_the_pingpong_tiles(dtype, causal, B, L, H, monkeypatch):
-    q, k, v = make_qkv(B, L, L, H, H, 128, dtype, seed=B + L)
+@pytest.mark.parametrize("causal,B,L,H,Hkv", [(False, 32, 512, 8, 8), (True, 8, 2048, 4, 4), (False, 16, 512, 16, 4),
+                                              (True, 8, 1536, 16, 4)],
+                         ids=["2-tiles", "causal-8-tiles", "gqa4-512", "gqa4-causal-1536"])
+def test_short_dense_rows_take_the_pingpong_tiles(dtype, causal, B, L, H, Hkv, monkeypatch):
+    q, k, v = make_qkv(B, L, L, H, Hkv, 128, dtype, seed=B + L)
     info = _kernel.launch_info(q, k, v, causal=causal)
     assert info.kernel_name.startswith(b"mfa_fwd16pp<"), info.kernel_name
     sel = [0, B - 1]  # the oracle on the first and the last sequence
@@ -84,7 +86,7 @@ def test_long_varlen_non_causal_takes_the_pingpong_tiles(dtype, monkeypatch):
                                    out_dtype=torch.float32)
     assert_parity(out32, ref, dtype, "varlen non-causal fp32 out")
     # causal: 4 query heads per K/V head pack into each ping-pong tile, so
-    # the longest sequence has 55 tiles of 64 positions (>= 16): ping-pong
+    # the longest sequence has 55 tiles of 64 positions (>= 20): ping-pong
     ran.clear()
     outc = mfa.flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens), max(lens), causal=True)
     assert ran and ran[-1].startswith(b"mfa_fwd16pp<"), ran
