@@ -2516,10 +2516,11 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             // vs 157; causal B=16 L=1024 113 vs 111, B=16 L=1536 221 vs 219,
             // B=8 L=2048 166 vs 176, B=4 L=3072 177 vs 180).  All 8 wavefronts of a ping-pong workgroup walk
             // the key range of all its 256 rows, so a sliding window must be
-            // wide against that: windows of >= 2048 keys run 3-13% faster there
-            // (L=8192 (1024,1024) 145 vs 154 us, (4096,0) causal 234 vs 241,
-            // L=32768 (2048,0) causal 610 vs 634), narrower ones 7-10% slower
-            // ((256,256) 67 vs 61, (512,0) causal 67 vs 61).  A soft-cap /
+            // wide against that: windows of >= 1536 keys (512 on packed
+            // grouped-query tiles, below) run faster there (L=8192
+            // (1024,1024) 145 vs 154 us, (4096,0) causal 234 vs 241, L=32768
+            // (2048,0) causal 610 vs 634), narrower ones slower ((256,256)
+            // 67 vs 61, (512,0) causal 67 vs 61).  A soft-cap /
             // ALiBi transform under a window stays on the 4-wavefront kernel
             // (L=32768 H=16 causal (2048,0) with soft-cap 30 and ALiBi: 832 vs
             // 791 us).  Varlen calls give only the longest sequence, and short
@@ -2560,8 +2561,14 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
             const int64_t min_tiles = packs              ? (min_pos + pos_pp - 1) / pos_pp
                                       : p->cu_seqlens_q ? (p->causal ? 16 : 5)
                                                         : (p->causal ? 8 : 2);
+            // Windows: re-measured on the current tiles (bf16, 4-wavefront vs
+            // ping-pong): unpacked L=8192 H=16 (512,511) 90.8 vs 90.4 us,
+            // (768,767) 122 vs 118, causal (1024,0) 89.3 vs 90.0, (1536,0)
+            // 119 vs 116; packed B=4 L=4096 Hq=32 Hkv=8 (256,256) 193 vs
+            // 184, (512,511) 310 vs 284, causal (1024,0) 297 vs 276.
+            const int64_t min_window = packs ? 512 : 1536;
             fills_chip = units_pp * t256 >= geom.cus && 4 * rows_pp <= 5 * rows_4w && t256 >= min_tiles &&
-                         (!windowed || (!bias && left + right + 1 >= 2048));
+                         (!windowed || (!bias && left + right + 1 >= min_window));
         } else
             fills_chip = units * (rows512 / 512) >= geom.cus && 4 * rows512 <= 5 * rows256;
     }

@@ -237,6 +237,17 @@ def test_launch_geometry_of_the_baseline_configs(lib):
     assert gqa(64, 256, False).startswith(b"mfa_fwd16<f16,d128")
     assert gqa(16, 1024, True).startswith(b"mfa_fwd16<f16,d128")
     assert gqa(12, 1536, True).startswith(b"mfa_fwd16pp<f16,d128")
+    # windows: >= 1536 keys wide, >= 512 on packed grouped-query tiles
+    q4 = torch.empty(4, 4096, 32, 128, dtype=torch.float16)
+    kv4 = torch.empty(4, 4096, 8, 128, dtype=torch.float16)
+    assert _kernel.launch_info(q4, kv4, kv4, window_left=256, window_right=256).kernel_name.startswith(
+        b"mfa_fwd16pp<f16,d128")
+    assert _kernel.launch_info(q4, kv4, kv4, window_left=200, window_right=200).kernel_name.startswith(
+        b"mfa_fwd16<f16,d128")
+    assert _kernel.launch_info(f16, f16, f16, window_left=768, window_right=767).kernel_name.startswith(
+        b"mfa_fwd16pp<f16,d128")
+    assert _kernel.launch_info(f16, f16, f16, window_left=512, window_right=511).kernel_name.startswith(
+        b"mfa_fwd16<f16,d128")
     small128 = torch.empty(1, 2048, 16, 128, dtype=torch.float16)
     assert _kernel.launch_info(small128, small128, small128).kernel_name.startswith(b"mfa_fwd16<f16,d128")
     big = torch.empty(1, 32768, 16, 128, dtype=torch.bfloat16)

@@ -1,6 +1,6 @@
 """Head dim 128 calls that the automatic choice sends to the ping-pong tiles
-because their key ranges are long: sliding windows of >= 2048 keys without a
-soft-cap / ALiBi transform, varlen calls whose longest sequence has >= 5
+because their key ranges are long: sliding windows of >= 1536 keys (512 on
+packed grouped-query tiles) without a soft-cap / ALiBi transform, varlen calls whose longest sequence has >= 5
 tiles (16 when causal) and dense rows of >= 2 tiles (8 when causal) -- of 256
 rows, or of 256 / R positions when the tiles pack R = 2, 4 or 8 query heads
 of one K/V head.  Each case checks the kernel the library picks
@@ -29,13 +29,15 @@ def _fp32_dense(q, k, v, causal, ws):
 
 
 @pytest.mark.parametrize("dtype", DTYPES16)
-@pytest.mark.parametrize("causal,ws,L,H", [
-    (False, (1024, 1023), 4096, 16),  # 2048 keys wide, both sides
-    (True, (2048, 0), 8192, 8),       # causal sliding window
-    (False, (2048, -1), 4096, 16),    # left bound only
-], ids=["both-sides", "causal", "left-only"])
-def test_wide_windows_take_the_pingpong_tiles(dtype, causal, ws, L, H, monkeypatch):
-    q, k, v = make_qkv(1, L, L, H, H, 128, dtype, seed=L + H + ws[0])
+@pytest.mark.parametrize("causal,ws,L,H,Hkv", [
+    (False, (1024, 1023), 4096, 16, 16),  # 2048 keys wide, both sides
+    (True, (2048, 0), 8192, 8, 8),        # causal sliding window
+    (False, (2048, -1), 4096, 16, 16),    # left bound only
+    (False, (768, 767), 4096, 16, 16),    # 1536 keys wide
+    (False, (256, 256), 4096, 32, 8),     # packed grouped-query tiles: 513 keys wide
+], ids=["both-sides", "causal", "left-only", "1536-wide", "packed-513-wide"])
+def test_wide_windows_take_the_pingpong_tiles(dtype, causal, ws, L, H, Hkv, monkeypatch):
+    q, k, v = make_qkv(1, L, L, H, Hkv, 128, dtype, seed=L + H + ws[0])
     info = _kernel.launch_info(q, k, v, causal=causal, window_left=ws[0], window_right=ws[1])
     assert info.kernel_name.startswith(b"mfa_fwd16pp<"), info.kernel_name
     kw = dict(causal=causal, window_size=ws)
