@@ -2594,11 +2594,20 @@ int make_plan(const mfa_fwd_params* p, Plan* plan, const ChipGeom& geom, int spl
     // faster than the 4-wavefront kernel at D=64: causal B=1 L=4096 H=16 101
     // -> 80 us, B=1 L=8192 H=8 187 -> 146; non-causal B=1 L=4096 H=16 100 ->
     // 83, B=1 L=8192 H=8 188 -> 156).
+    // Shorter rows (2-3 tiles of 256) take those tiles too when they make
+    // 3/4 to one round of workgroups (bf16 H=8, 4-wavefront vs ping-pong:
+    // D=64 B=12 L=512 18.2 vs 16.7 us, B=16 L=512 18.8 vs 17.3, B=10 L=768
+    // 24.0 vs 21.9, causal B=16 L=512 21.3 vs 18.4; D=32 B=16 L=512 causal
+    // 17.7 vs 16.1; just past one round they lose: D=64 B=18 L=512 25.1 vs
+    // 30.4, B=11 L=768 33.5 vs 39.6).
+    const int64_t t256 = rows256 / 256, n256 = units * t256;
+    const bool one_round = t256 >= 2 && 4 * n256 >= 3 * (int64_t)geom.cus && n256 <= geom.cus &&
+                           4 * rows256 <= 5 * (int64_t)p->seqlen_q;
     if (p->tile_hint == MFA_TILE_AUTO && !fills_chip && !paged && split_keys == 0 && dp <= 64 &&
         din != MFA_DTYPE_F32 && !bias && !p->cu_seqlens_q && p->window_left < 0 && p->window_right < 0 &&
-        units * (rows256 / 256) >= geom.cus && rows256 / 256 >= 4) {
-        // (rows of >= 4 tiles: shorter rows, e.g. B=64 L=256 H=16, run 40 vs
-        // 50 us on the 4-wavefront kernel)
+        ((n256 >= geom.cus && t256 >= 4) || one_round)) {
+        // (rows of >= 4 tiles over more rounds: shorter rows, e.g. B=64
+        // L=256 H=16, run 40 vs 50 us on the 4-wavefront kernel)
         fills_chip = true;
         pp256 = true;
     } else if (p->tile_hint == MFA_TILE_AUTO && fills_chip && dp <= 64 && din != MFA_DTYPE_F32) {

@@ -198,6 +198,14 @@ def test_launch_geometry_of_the_baseline_configs(lib):
         assert _kernel.launch_info(c512, c512, c512).block_x == 256
         one_round = torch.empty(32, 512, 8, D, dtype=torch.bfloat16)  # 256 tiles of 512 rows, causal
         assert _kernel.launch_info(one_round, one_round, one_round, causal=True).block_x == 256
+        # 3/4 to one round of 256-row tiles: the 256-row ping-pong tiles
+        for B, L, causal in ((16, 512, False), (12, 512, True), (10, 768, False)):
+            t = torch.empty(B, L, 8, D, dtype=torch.bfloat16)
+            li = _kernel.launch_info(t, t, t, causal=causal)
+            assert li.block_x == 512 and li.rows_per_block == 256, (B, L, causal, li.kernel_name)
+        for B, L in ((18, 512), (11, 768), (8, 512)):  # past one round; under 3/4 of one
+            t = torch.empty(B, L, 8, D, dtype=torch.bfloat16)
+            assert _kernel.launch_info(t, t, t).block_x == 256, (B, L)
     c16k = torch.empty(1, 16384, 16, 64, dtype=torch.bfloat16)  # 512 tiles: balanced by the schedule
     assert _kernel.launch_info(c16k, c16k, c16k, causal=True).rows_per_block == 512
     f16 = torch.empty(1, 8192, 16, 128, dtype=torch.float16)
